@@ -1,0 +1,176 @@
+#!/usr/bin/env python
+"""Benchmark: DeepSeek-V3.2-shape sparse MLA decode on one MI355X.
+
+Workload (default ``mla_decode_b64_h128_k2048``): B=64 sequences, one query
+row each, H=128 heads, d_qk=576 (512 latent + 64 rope), d_v=512, bf16 q and
+paged KV (block 64) ~ N(0,1)*0.5, ctx 32768, top-k 2048 rows per query, no
+sink; split-KV schedule + LSE merge. A "step" is one call (attention kernel +
+merge kernel) over one input set. Four independent input sets (own pool,
+block tables, top-k sets, q) rotate so the 256 MB Infinity Cache cannot hold
+the gathered rows between calls. Inputs are resident in HBM and the schedule
+is precomputed before the timed region.
+
+Prints one JSON line. ``value`` is TFLOP/s of the whole call; the
+``roofline`` object rates the attention kernel alone: algorithmic bytes per
+launch / its mean duration (HIP events around each launch in the timed loop)
+against 8 TB/s HBM. ``cpu_baseline`` times the CPU restatement of the
+reference's golden math on this host over all query rows of one input set.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("sparse-attn decode TFLOP/s + gathered-KV HBM GB/s (% roofline), µs/call")
+HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2516.6     # MI355X dense bf16 MFMA
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="mla_decode_b64_h128_k2048")
+    ap.add_argument("--sets", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(inputs, counts):
+    """Golden-faithful CPU restatement (oracle/) over every query row of one input set."""
+    import torch
+
+    from oracle.golden_ref import attend_token, token_rows
+    from sparse_attn_sharedkv_amd.workloads import flops_and_bytes
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    kw = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inputs.items()}
+    q = kw["q"]
+    b_n, s_q = q.shape[0], q.shape[1]
+    lens = kw["seqused_kv"].tolist()
+    idx = kw["cmp_sparse_indices"]
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for b in range(b_n):
+            for s in range(s_q):
+                ori, cmp = token_rows(
+                    b=b, s=s, act_q=s_q, act_kv=lens[b], ori_kv=kw["ori_kv"],
+                    ori_block_table=kw["ori_block_table"], cmp_kv=kw["cmp_kv"],
+                    cmp_block_table=kw["cmp_block_table"],
+                    cmp_idx_row=None if idx is None else idx[b, s, 0].tolist(),
+                    cmp_ratio=kw["cmp_ratio"], ori_win_left=kw["ori_win_left"])
+                attend_token(q[b, s], [ori, cmp], kw["sinks"], kw["softmax_scale"],
+                             d_v=kw["head_dim_v"])
+        times.append(time.perf_counter() - t0)
+    sec = sorted(times)[1]
+    flops, _ = flops_and_bytes(counts)
+    return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "us_per_call": round(sec * 1e6, 1),
+            "sample": f"all {counts['tokens']} query rows of one input set (paged gather + "
+                      f"512-row online softmax, torch fp32), median of 3"}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE={world})", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from sparse_attn_sharedkv_amd import api
+    from sparse_attn_sharedkv_amd.workloads import (WORKLOADS, build_workload, flops_and_bytes,
+                                                    workload_counts)
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = WORKLOADS[args.workload]
+    sets = [build_workload(args.workload, device=dev, seed=100 + i) for i in range(args.sets)]
+    counts = workload_counts(sets[0])
+    flops, nbytes = flops_and_bytes(counts)
+    preps = []
+    for kw in sets:
+        call = {k: v for k, v in kw.items()}
+        preps.append(api.prepare(**call))
+    torch.cuda.synchronize()
+
+    k, wu = args.steps, args.warmup
+    for i in range(wu):
+        api.launch(preps[i % len(preps)])
+    torch.cuda.synchronize()
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * k + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev[0].record()
+    for i in range(k):
+        p = preps[i % len(preps)]
+        api.launch(p, phases=1)
+        ev[2 * i + 1].record()
+        api.launch(p, phases=2)
+        ev[2 * i + 2].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = ev[0].elapsed_time(ev[2 * k])
+    attn_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(k)]
+    merge_ms = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(k)]
+    ms_step = total_ms / k
+    attn_avg = sum(attn_ms) / k
+    merge_avg = sum(merge_ms) / k
+    srt = sorted(attn_ms)
+
+    achieved = nbytes / (attn_avg * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": round(flops / (ms_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": k,
+        "warmup": wu,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "batch": w["B"], "s_q": w["S"], "heads": w["H"],
+                   "d_qk": w["D"], "d_v": w["DV"], "topk": w["K"], "ctx": list(w["ctx"]),
+                   "block_size": 64, "input_sets": len(preps), "tokens": counts["tokens"],
+                   "attended_rows": counts["rows"]},
+        "us_per_call": round(ms_step * 1e3, 2),
+        "gathered_kv_GBps_call": round(counts["rows"] * counts["d_qk"] * 2 / (ms_step * 1e-3)
+                                       / 1e9, 1),
+        "hbm_roofline_frac_call": round(nbytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "mfma_frac_call": round(flops / (ms_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "attn_kernel_us": {"mean": round(attn_avg * 1e3, 2), "p10": round(srt[k // 10] * 1e3, 2),
+                           "p50": round(srt[k // 2] * 1e3, 2),
+                           "p90": round(srt[(9 * k) // 10] * 1e3, 2)},
+        "merge_kernel_us": round(merge_avg * 1e3, 2),
+        "host_wall_us_per_step": round(wall / k * 1e6, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "algorithmic_bytes": int(nbytes),
+                     "kernel": "sas::attn_kernel"},
+        "peaks": {"hbm_GBps": HBM_PEAK_GBPS, "bf16_mfma_TFLOPs": BF16_PEAK_TFLOPS},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(sets[0], counts)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+/*
+ * sas_mi355x.h - C ABI of the MI355X (gfx950) sparse shared-KV attention library.
+ *
+ * Plain pointers and sizes only; no torch or HIP C++ types beyond hipStream_t
+ * (passed as void*). Every entry point returns 0 on success or a negative
+ * SAS_E* code; sas_last_error() returns a message for the calling thread.
+ *
+ * Reference interfaces replaced (yangqiang2018/sparse_attn_sharedkv):
+ *   sas_metadata_build     <- metadata.sparse_attn_sharedkv_metadata  (metadata.py:1018-1086)
+ *                             (port of the AICPU SparseAttnSharedkvMetadata scheduler)
+ *   sas_attention_launch   <- the JIT kernel callable built by build_sparse_attn_sharedkv
+ *                             func(Q, ori_kv, ori_block_table, cmp_kv, cmp_block_table,
+ *                                  cmp_indices, q_prefix, act_q_lens, seqused_kv, sinks,
+ *                                  metadata) -> (Output, LSE)          (kernel.py:73-183, :353-382;
+ *                             api.py:372-384 is the call site); the metadata-free twin
+ *                             build_sparse_flash_mla (sparse_flash_mla_kernel.py:19-107, :189-210)
+ *                             maps onto the same entry point with metadata built by the host.
+ *   sas_workspace_bytes    <- workspace_idx auto-allocation of the JIT (kernel.py:353-382): the
+ *                             caller allocates the split-KV partial buffer instead.
+ */
+#ifndef SAS_MI355X_H_
+#define SAS_MI355X_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- metadata layout (int32 words) -------------------------------------
+ * FA rows ("virtual cores" = workgroups of the attention kernel), 8 words each,
+ * same field order as metadata.py:45-52:
+ *   [enable, bn2_start, m_start, s2_start, bn2_end, m_end, s2_end, first_partial_slot]
+ * An item is (bn2 = batch, m = m-block): m-block m of batch b is query row
+ * m / HB of that batch, heads [(m % HB) * m_base, +m_base) with
+ * HB = ceil(num_heads / m_base) (the reference's s1g blocks of mBaseSize,
+ * metadata.py:388, :676-679). A row covers the items from
+ * (bn2_start, m_start) block s2_start up to, excluding, (bn2_end, m_end)
+ * block s2_end; s2 counts SAS blocks of s2_base positions over the item's
+ * attended list [window rows ++ compressed positions].
+ * FD rows (split-KV merge tasks), 8 words each, field order of metadata.py:54-60:
+ *   [enable, bn2_idx, m_idx, partial_slot_first, partial_count, head_start, head_count, 0]
+ * (head_start / head_count are relative to the item's m-block, as fd_m_start / fd_m_num).
+ * Config row (last 8 words): [SAS_META_MAGIC, s2_base, num_fa, num_fd,
+ *                             num_partial_slots, num_heads, m_base, total_items]
+ */
+#define SAS_AIC_CORE_NUM 512
+#define SAS_AIV_CORE_NUM 1024
+#define SAS_FA_METADATA_SIZE 8
+#define SAS_FD_METADATA_SIZE 8
+#define SAS_FD_OFFSET (SAS_AIC_CORE_NUM * SAS_FA_METADATA_SIZE)
+#define SAS_META_SIZE 16384
+#define SAS_CFG_OFFSET (SAS_META_SIZE - 8)
+#define SAS_META_MAGIC 0x5A53A355
+
+/* ---- error codes ---- */
+#define SAS_OK 0
+#define SAS_E_INVALID (-1)     /* bad argument (shape, pointer, scenario)      */
+#define SAS_E_UNSUPPORTED (-2) /* combination this build has no kernel for     */
+#define SAS_E_CAPACITY (-3)    /* schedule does not fit the metadata capacity  */
+#define SAS_E_HIP (-4)         /* HIP runtime error (launch or attribute call) */
+
+/* Scenario codes (api.py:196-202): 1 = SWA, 2 = CFA (dense compressed), 3 = SCFA (top-k). */
+
+/* Host-side scheduler (no GPU needed). Fills meta_out[SAS_META_SIZE].
+ * act_q[b]: query rows of batch b; act_kv[b]: raw KV length of batch b.
+ * m_base: heads per item (32 when num_heads <= 32, else 64).
+ * num_cores: workgroups to balance over (<= SAS_AIC_CORE_NUM).
+ * s2_base: positions per schedulable block (multiple of 32).
+ * min_split_blocks: an item is split across workgroups only into pieces of at
+ * least this many blocks. fd_head_chunk: heads per merge task.
+ * Returns the number of FA rows used (>= 1) or a negative error code. */
+int sas_metadata_build(int32_t* meta_out, int batch, const int32_t* act_q,
+                       const int32_t* act_kv, int num_heads, int m_base, int ori_win_left,
+                       int scenario, int cmp_ratio, int cmp_topk, int num_cores,
+                       int s2_base, int min_split_blocks, int fd_head_chunk);
+
+/* Bytes of split-KV partial workspace for a schedule:
+ * num_partial_slots * m_base * (head_dim_v + 1) * sizeof(float). */
+int64_t sas_workspace_bytes(int num_partial_slots, int m_base, int head_dim_v);
+
+/* dtype codes */
+#define SAS_DTYPE_BF16 0
+#define SAS_DTYPE_FP16 1
+
+typedef struct SasAttnArgs {
+  /* inputs (device pointers) */
+  const void* q;                 /* [total_tokens, num_heads, head_dim] dtype                 */
+  const void* ori_kv;            /* [ori_block_num, ori_block_size, 1, head_dim] dtype         */
+  const int32_t* ori_block_table;/* [batch, ori_table_len]                                     */
+  const void* cmp_kv;            /* [cmp_block_num, cmp_block_size, 1, head_dim] or NULL        */
+  const int32_t* cmp_block_table;/* [batch, cmp_table_len] or NULL                             */
+  const int32_t* cmp_indices;    /* [total_tokens, 1, topk] (scenario 3) or NULL               */
+  const int32_t* q_prefix;       /* [batch] first flat token of each batch                     */
+  const int32_t* act_q_lens;     /* [batch]                                                    */
+  const int32_t* seqused_kv;     /* [batch]                                                    */
+  const float* sinks;            /* [num_heads] fp32 (may hold -inf)                           */
+  const int32_t* metadata;       /* [SAS_META_SIZE] from sas_metadata_build                    */
+  /* outputs (device pointers) */
+  void* out;                     /* [total_tokens, num_heads, head_dim_v] dtype                */
+  float* lse;                    /* [total_tokens, num_heads] fp32                             */
+  float* workspace;              /* sas_workspace_bytes(...) bytes, or NULL if num_fd == 0     */
+  /* sizes */
+  int32_t batch, total_tokens, num_heads, head_dim, head_dim_v;
+  int32_t ori_block_num, ori_block_size, ori_table_len;
+  int32_t cmp_block_num, cmp_block_size, cmp_table_len, topk;
+  int32_t scenario, cmp_ratio, ori_win_left, dtype;
+  float softmax_scale;
+  /* schedule summary (copies of the metadata config row, known to the host) */
+  int32_t num_fa, num_fd, num_partial_slots, s2_base, m_base;
+  /* kernels to enqueue: bit 0 attention, bit 1 split-KV merge; 0 means both.
+   * A caller may enqueue the two phases as separate calls (attention first). */
+  int32_t phases;
+} SasAttnArgs;
+
+/* Launch the attention kernel and, when num_fd > 0, the split-KV merge kernel on
+ * `stream` (a hipStream_t). Asynchronous; no allocation, no host synchronisation. */
+int sas_attention_launch(const SasAttnArgs* args, void* stream);
+
+/* Library version (major * 100 + minor). */
+int sas_version(void);
+
+/* sizeof(SasAttnArgs) as compiled into the library (binding layout check). */
+int sas_args_struct_size(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* sas_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAS_MI355X_H_ */

@@ -1,0 +1,307 @@
+"""Host entry point ``sparse_attn_sharedkv`` (signature and behaviour of api.py:129-397).
+
+Scenario detection (api.py:196-202):
+
+* ``cmp_kv=None, cmp_sparse_indices=None`` -> SWA (scenario 1)
+* ``cmp_kv=<tensor>, cmp_sparse_indices=None`` -> CFA (scenario 2)
+* ``cmp_kv=<tensor>, cmp_sparse_indices=<tensor>`` -> SCFA (scenario 3)
+
+Q / indices are flattened to ``[total_tokens, ...]`` with a per-batch
+``q_prefix`` exactly as api.py:208-240 does (TND passes through, BSND is a
+free reshape). The paged caches go to the GPU untouched; the HIP kernels
+resolve block tables on the device. Additions over the reference, all
+optional and defaulting to its behaviour: ``head_dim_v`` (output width; the
+first ``head_dim_v`` columns of each shared row are V, as in MLA where
+d_qk = 576 and d_v = 512), and head counts other than 64 (multiples of 16 up
+to 128).
+
+Errors follow the reference: AssertionError for unsupported masks / layouts,
+missing ``cu_seqlens_q`` in TND, top-k length mismatch and metadata size;
+ValueError for dtypes and shapes; RuntimeError (with the library's message)
+for launch failures. Everything is checked on the host before any launch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+from dataclasses import dataclass, field
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+from .metadata import (DEFAULT_CORE_NUM, SAS_META_SIZE, build_metadata, config_row,  # noqa: F401
+                       m_base_for)
+
+DEFAULT_BLOCK_I = 128  # kernel.py:65, kept for callers that import it
+SUPPORTED_HEAD_DIMS = (512, 576)
+SUPPORTED_HEAD_DIM_V = (512,)
+
+
+def _dtype_code(t: torch.dtype) -> int:
+    if t == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if t == torch.float16:
+        return _lib.DTYPE_FP16
+    raise ValueError(f"unsupported torch dtype {t}")
+
+
+@dataclass
+class Prepared:
+    """A fully validated call: device tensors, launch arguments, output views."""
+
+    args: _lib.SasAttnArgs
+    keep: list = field(default_factory=list)   # tensors that must outlive the launch
+    out: Optional[torch.Tensor] = None
+    lse: Optional[torch.Tensor] = None
+    layout_q: str = "TND"
+    bsnd_shape: Optional[tuple] = None
+    device: Optional[torch.device] = None
+
+
+@functools.lru_cache(maxsize=64)
+def _cached_schedule(act_q: tuple, act_kv: tuple, num_heads: int, ori_win_left: int,
+                     scenario: int, cmp_ratio: int, topk: int, core_num: int) -> torch.Tensor:
+    return build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads,
+                          ori_win_left=ori_win_left, scenario=scenario, cmp_ratio=cmp_ratio,
+                          cmp_topk=topk, core_num=core_num)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Tensor] = None,
+            cmp_sparse_indices: Optional[torch.Tensor] = None, ori_block_table: torch.Tensor,
+            cmp_block_table: Optional[torch.Tensor] = None,
+            cu_seqlens_q: Optional[torch.Tensor] = None,
+            seqused_q: Optional[torch.Tensor] = None, seqused_kv: torch.Tensor,
+            sinks: torch.Tensor, metadata: Optional[torch.Tensor] = None,
+            softmax_scale: float, cmp_ratio: Optional[int] = None, ori_mask_mode: int = 4,
+            cmp_mask_mode: int = 3, ori_win_left: int = 127, ori_win_right: int = 0,
+            layout_q: str = "TND", layout_kv: str = "PA_ND",
+            core_num: int = DEFAULT_CORE_NUM, topk_cmp: Optional[int] = None,
+            head_dim_v: Optional[int] = None) -> Prepared:
+    """Validate and stage one call (host work of api.py:186-384) without launching."""
+    del seqused_q  # API-parity placeholder (api.py:186)
+    assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
+    assert cmp_mask_mode == 3 or cmp_kv is None, "only cmp_mask_mode=3 supported"
+    assert ori_win_right == 0, "only ori_win_right=0 supported"
+    assert layout_kv == "PA_ND", "only layout_kv=PA_ND supported"
+    assert layout_q in ("TND", "BSND"), f"unsupported layout_q={layout_q!r}"
+
+    dtype = q.dtype
+    dcode = _dtype_code(dtype)
+    if cmp_kv is None:
+        scenario = 1
+    elif cmp_sparse_indices is None:
+        scenario = 2
+    else:
+        scenario = 3
+
+    # ---- flatten Q / indices to [total_tokens, ...] (api.py:208-240) ----
+    cu_host = None
+    if layout_q == "TND":
+        assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
+        if q.dim() != 3:
+            raise ValueError(f"TND q must be [T, N1, D], got {tuple(q.shape)}")
+        cu_host = [int(x) for x in cu_seqlens_q.to(torch.int32).cpu().tolist()]
+        nb = len(cu_host) - 1
+        act_q = [cu_host[i + 1] - cu_host[i] for i in range(nb)]
+        t1, n1, d = q.shape
+        total = t1
+        prefix = cu_host[:-1]
+        padded = (cu_host[-1] != t1) if cu_host else t1 > 0
+    else:
+        if q.dim() != 4:
+            raise ValueError(f"BSND q must be [B, S, N1, D], got {tuple(q.shape)}")
+        nb, s_max, n1, d = q.shape
+        total = nb * s_max
+        prefix = [i * s_max for i in range(nb)]
+        act_q = [s_max] * nb
+        padded = False
+        if cu_seqlens_q is not None:
+            cu_host = [int(x) for x in cu_seqlens_q.to(torch.int32).cpu().tolist()]
+            act_q = [cu_host[i + 1] - cu_host[i] for i in range(nb)]
+            padded = any(a != s_max for a in act_q)
+
+    idx_flat = None
+    k = 0
+    if scenario == 3:
+        ci = cmp_sparse_indices
+        if ci.dim() != (3 if layout_q == "TND" else 4):
+            raise ValueError(f"cmp_sparse_indices has rank {ci.dim()} for layout {layout_q}")
+        idx_flat = ci.reshape(total, ci.shape[-2], ci.shape[-1])
+        n2 = idx_flat.shape[1]
+        k = topk_cmp if topk_cmp is not None else idx_flat.shape[2]
+        assert k == idx_flat.shape[2], "topk_cmp does not match cmp_sparse_indices last dim"
+    elif scenario == 2:
+        n2 = cmp_kv.shape[2]
+    else:
+        n2 = ori_kv.shape[2]
+
+    dv = d if head_dim_v is None else int(head_dim_v)
+    if n2 != 1 or ori_kv.shape[2] != 1 or ori_kv.shape[-1] != d:
+        raise ValueError(f"only N2=1 shared KV with KV width == q width supported "
+                         f"(got N2={n2}, q D={d}, kv {tuple(ori_kv.shape)})")
+    if d not in SUPPORTED_HEAD_DIMS or dv not in SUPPORTED_HEAD_DIM_V or dv > d:
+        raise ValueError(f"supported head dims: D in {SUPPORTED_HEAD_DIMS} with head_dim_v in "
+                         f"{SUPPORTED_HEAD_DIM_V} (got D={d}, head_dim_v={dv})")
+    if n1 < 16 or n1 > 128 or n1 % 16 != 0:
+        raise ValueError(f"N1 must be a multiple of 16 in [16, 128] (got N1={n1})")
+    if ori_kv.dtype != dtype or (cmp_kv is not None and cmp_kv.dtype != dtype):
+        raise ValueError("KV caches must have q's dtype")
+    if ori_win_left < -1:
+        raise ValueError("ori_win_left must be >= -1")
+    if scenario >= 2:
+        if cmp_block_table is None:
+            raise ValueError("cmp_block_table is required with cmp_kv")
+        if cmp_ratio is not None and cmp_ratio < 1:
+            raise ValueError("cmp_ratio must be >= 1")
+        if cmp_kv.shape[-1] != d or cmp_kv.shape[2] != 1:
+            raise ValueError("cmp_kv must be [blocks, block_size, 1, D]")
+    cmp_ratio_eff = int(cmp_ratio) if cmp_ratio is not None else 4  # api.py:287
+    if metadata is not None:
+        assert metadata.numel() == SAS_META_SIZE, (
+            f"metadata must have {SAS_META_SIZE} int32 entries (got {metadata.numel()})")
+
+    dev = q.device
+    if dev.type != "cuda":
+        raise RuntimeError("sparse_attn_sharedkv runs on a ROCm GPU; q is on " + str(dev))
+
+    # ---- schedule (api.py:335-366) ----
+    if metadata is None:
+        kv_host = tuple(int(x) for x in seqused_kv.to(torch.int32).cpu().tolist())
+        md = _cached_schedule(tuple(act_q), kv_host, int(n1), int(ori_win_left), scenario,
+                              cmp_ratio_eff, int(k), int(core_num))
+        cfg = config_row(md)
+        metadata_dev = md.to(dev, non_blocking=True)
+    else:
+        metadata_dev = metadata.to(dev).to(torch.int32).reshape(SAS_META_SIZE).contiguous()
+        cfg = config_row(metadata)  # host read of the schedule summary row
+        assert cfg["num_heads"] == n1 and cfg["m_base"] == m_base_for(n1), (
+            "metadata was built for a different head count")
+
+    # ---- device tensors ----
+    i32 = torch.int32
+    q_flat = q.reshape(total, n1, d).contiguous()
+    ori_kv_d = ori_kv.contiguous()
+    ori_bt = ori_block_table.to(device=dev, dtype=i32).contiguous()
+    cmp_kv_d = cmp_kv.contiguous() if cmp_kv is not None else None
+    cmp_bt = cmp_block_table.to(device=dev, dtype=i32).contiguous() if cmp_kv is not None else None
+    idx_d = idx_flat.to(device=dev, dtype=i32).contiguous() if idx_flat is not None else None
+    q_prefix = torch.tensor(prefix, dtype=i32).to(dev, non_blocking=True)
+    act_q_d = torch.tensor(act_q, dtype=i32).to(dev, non_blocking=True)
+    seqused = seqused_kv.to(device=dev, dtype=i32).contiguous()
+    sinks_d = sinks.to(device=dev, dtype=torch.float32).contiguous()
+    if sinks_d.numel() != n1:
+        raise ValueError(f"sinks must have N1={n1} entries")
+    alloc = torch.zeros if padded else torch.empty
+    out = alloc((total, n1, dv), dtype=dtype, device=dev)
+    lse = alloc((total, n1), dtype=torch.float32, device=dev)
+    ws = None
+    if cfg["num_fd"] > 0:
+        nbytes = _lib.load().sas_workspace_bytes(cfg["num_partial_slots"], cfg["m_base"], dv)
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+
+    for t in (q_flat, ori_kv_d, cmp_kv_d):
+        if t is not None and t.device != dev:
+            raise ValueError("all tensors must be on q's device")
+
+    a = _lib.SasAttnArgs()
+    a.q, a.ori_kv, a.ori_block_table = _ptr(q_flat), _ptr(ori_kv_d), _ptr(ori_bt)
+    a.cmp_kv, a.cmp_block_table, a.cmp_indices = _ptr(cmp_kv_d), _ptr(cmp_bt), _ptr(idx_d)
+    a.q_prefix, a.act_q_lens, a.seqused_kv = _ptr(q_prefix), _ptr(act_q_d), _ptr(seqused)
+    a.sinks, a.metadata = _ptr(sinks_d), _ptr(metadata_dev)
+    a.out, a.lse, a.workspace = _ptr(out), _ptr(lse), _ptr(ws)
+    a.batch, a.total_tokens, a.num_heads = nb, total, n1
+    a.head_dim, a.head_dim_v = d, dv
+    a.ori_block_num, a.ori_block_size, a.ori_table_len = (
+        ori_kv_d.shape[0], ori_kv_d.shape[1], ori_bt.shape[1])
+    if cmp_kv_d is not None:
+        a.cmp_block_num, a.cmp_block_size, a.cmp_table_len = (
+            cmp_kv_d.shape[0], cmp_kv_d.shape[1], cmp_bt.shape[1])
+    a.topk = int(k)
+    a.scenario, a.cmp_ratio, a.ori_win_left, a.dtype = scenario, cmp_ratio_eff, ori_win_left, dcode
+    a.softmax_scale = float(softmax_scale)
+    a.num_fa, a.num_fd = cfg["num_fa"], cfg["num_fd"]
+    a.num_partial_slots, a.s2_base, a.m_base = (
+        cfg["num_partial_slots"], cfg["s2_base"], cfg["m_base"])
+    keep = [q_flat, ori_kv_d, ori_bt, cmp_kv_d, cmp_bt, idx_d, q_prefix, act_q_d, seqused,
+            sinks_d, metadata_dev, out, lse, ws]
+    return Prepared(args=a, keep=keep, out=out, lse=lse, layout_q=layout_q,
+                    bsnd_shape=None if layout_q == "TND" else (nb, total // max(nb, 1), n1, dv),
+                    device=dev)
+
+
+def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: int = 0) -> None:
+    """Enqueue the attention (+ merge) kernels on ``stream`` (default: current stream).
+
+    ``phases``: 0 both kernels, 1 the attention kernel only, 2 the merge only
+    (a caller timing the two kernels separately enqueues 1 then 2).
+    """
+    lib = _lib.load()
+    st = stream if stream is not None else torch.cuda.current_stream(prep.device)
+    prep.args.phases = int(phases)
+    rc = lib.sas_attention_launch(ctypes.byref(prep.args), ctypes.c_void_p(st.cuda_stream))
+    if rc != _lib.SAS_OK:
+        raise RuntimeError(_lib.last_error())
+
+
+def finalize(prep: Prepared, return_softmax_lse: bool):
+    """Restore the caller's layout (api.py:386-397)."""
+    out, lse = prep.out, prep.lse
+    if prep.layout_q == "BSND":
+        b, s, n1, dv = prep.bsnd_shape
+        out = out.reshape(b, s, n1, dv)
+        lse = lse.reshape(b, s, n1)
+    if return_softmax_lse:
+        return out, lse
+    return out
+
+
+def sparse_attn_sharedkv(
+    q: torch.Tensor,
+    *,
+    ori_kv: torch.Tensor,
+    cmp_kv: Optional[torch.Tensor] = None,
+    cmp_sparse_indices: Optional[torch.Tensor] = None,
+    ori_block_table: torch.Tensor,
+    cmp_block_table: Optional[torch.Tensor] = None,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    seqused_q: Optional[torch.Tensor] = None,
+    seqused_kv: torch.Tensor,
+    sinks: torch.Tensor,
+    metadata: Optional[torch.Tensor] = None,
+    softmax_scale: float,
+    cmp_ratio: Optional[int] = None,
+    ori_mask_mode: int = 4,
+    cmp_mask_mode: int = 3,
+    ori_win_left: int = 127,
+    ori_win_right: int = 0,
+    layout_q: str = "TND",
+    layout_kv: str = "PA_ND",
+    return_softmax_lse: bool = False,
+    core_num: int = DEFAULT_CORE_NUM,
+    topk_cmp: Optional[int] = None,
+    head_dim_v: Optional[int] = None,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Sparse shared-KV attention forward; returns ``attention_out`` in q's layout.
+
+    With ``return_softmax_lse=True`` returns ``(attention_out, lse)``, lse fp32
+    ``[T1, N1]`` (TND) or ``[B, S1, N1]`` (BSND), ``lse = max + ln(sum)`` over
+    all attended keys with the sink folded in (api.py:176-184). ``metadata``
+    is the output of ``sparse_attn_sharedkv_metadata``; when omitted it is
+    built here from the inputs (api.py:335-360).
+    """
+    prep = prepare(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
+                   ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
+                   cu_seqlens_q=cu_seqlens_q, seqused_q=seqused_q, seqused_kv=seqused_kv,
+                   sinks=sinks, metadata=metadata, softmax_scale=softmax_scale,
+                   cmp_ratio=cmp_ratio, ori_mask_mode=ori_mask_mode,
+                   cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
+                   ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
+                   core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v)
+    launch(prep)
+    return finalize(prep, return_softmax_lse)

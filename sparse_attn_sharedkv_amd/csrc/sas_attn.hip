@@ -1,0 +1,655 @@
+// Sparse shared-KV attention decode for MI355X (gfx950 / CDNA4).
+//
+// Replaces the reference's fused TileLang kernels (kernel.py:_build_swa /
+// _build_cfa / _build_scfa and sparse_flash_mla_kernel.py:_build_swa/_hca/_csa)
+// with one metadata-driven HIP kernel plus a split-KV merge kernel.
+//
+// Work decomposition
+//   One workgroup per FA metadata row; it walks its items (query rows) and,
+//   inside each, its blocks of the attended list [window rows ++ compressed
+//   positions]. All query heads of a token share every gathered KV row
+//   (shared KV, N2 = 1): a 32-row tile is loaded once into LDS and read by
+//   every wave, as K for Q·Kᵀ and (first head_dim_v columns) as V for P·V.
+//
+// Waves (NHG head groups of 32 heads; 2*NHG waves):
+//   wave w -> head group hg = w % NHG, half p = w / NHG.
+//   Q·Kᵀ: wave computes Sᵀ[32 rows x 32 heads] over dims half p of d_qk with
+//         v_mfma_f32_32x32x16 (A = K rows from LDS, B = Qᵀ held in VGPRs);
+//         the two halves of a head group are summed through LDS.
+//   softmax: each lane owns one head (lane % 32) and 16 of the 32 rows; the
+//         other 16 live in lane ^ 32. exp2 domain, lazy rescaling (the O
+//         rescale only runs when some head's max grows by > 2^8).
+//   P·V:  wave accumulates Oᵀ[dv half p x 32 heads] with the same MFMA
+//         (A = Vᵀ via ds_read_b64_tr_b16 from the row-major tile, B = Pᵀ
+//         straight from the Sᵀ accumulator layout, no data movement).
+//
+// Gather: global_load_lds_dwordx4 (16 B per lane straight into LDS, no VGPR
+//   staging) into a 3-stage ring; rows of a tile are rotated by 16-byte
+//   chunks so both the Kᵀ reads (b128) and the transposed V reads (tr_b16)
+//   are bank-conflict free.
+//
+// Numerics follow golden.py:156-200: fp32 scores, P rounded to the input
+// dtype before P·V while the running sum uses fp32 P, out = acc / l rounded
+// RNE, lse = m + ln(l). Split pieces emit (acc / l, lse) without the sink;
+// the merge adds the sink once.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/sas_mi355x.h"
+#include "sas_items.h"
+
+namespace sas {
+
+static thread_local std::string g_last_error;
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define SAS_LDS __attribute__((address_space(3)))
+
+constexpr int TILE = 32;        // KV rows per pipeline stage
+constexpr int NSTAGE = 3;       // LDS ring depth
+constexpr int RCHUNK = 1024;    // positions resolved into LDS at a time
+constexpr uint32_t ROW_INVALID = 0xFFFFFFFFu;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+constexpr float RESCALE_TAU = 8.0f;  // lazy-rescale threshold (log2 units)
+
+template <typename T> struct MfmaOps;
+template <> struct MfmaOps<__bf16> {
+  typedef bf16x8 vec8;
+  static __device__ inline f32x16 mma(i16x8 a, i16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ inline short from_f32(float x) {
+    return __builtin_bit_cast(short, (__bf16)x);
+  }
+};
+template <> struct MfmaOps<_Float16> {
+  typedef f16x8 vec8;
+  static __device__ inline f32x16 mma(i16x8 a, i16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ inline short from_f32(float x) {
+    return __builtin_bit_cast(short, (_Float16)x);
+  }
+};
+
+// LDS stage layout (one 32-row tile).
+//   main part, dims 0..511: row r occupies MAIN_SLOTS = 68 sixteen-byte slots
+//     (1088 B); its chunk c (dims 8c..8c+7) sits in slot c + rot(r) with
+//     rot(r) = (r >> 2) & 3. One DMA instruction (64 lanes x 16 B) fills one
+//     row, and every read address is one per-lane base plus an immediate.
+//   rope part, dims 512..575 (head_dim 576): 8 slots per row after the main
+//     part; chunk 64 + c' of row r sits in slot 8 r + ((c' + (r >> 1)) & 7), so
+//     one DMA instruction fills 8 rows.
+// With 64 banks x 4 B (16 sixteen-byte bank groups):
+//   * Kᵀ reads (ds_read_b128, 16 lanes = rows r..r+15 at one chunk) hit bank
+//     groups (4 r + rot(r) + c) mod 16 (main) or (8 r + ((c' + r/2) & 7)) mod 16
+//     (rope), all distinct;
+//   * Vᵀ reads (ds_read_b64_tr_b16, 32 lanes = 4 consecutive rows x 4 chunks)
+//     start at 4 (r % 4) + rot(r) = {0, 4, 8, 12} + const, four disjoint spans.
+constexpr int MAIN_SLOTS = 68;
+constexpr int MAIN_ROW_BYTES = MAIN_SLOTS * 16;
+constexpr int MAIN_BYTES = TILE * MAIN_ROW_BYTES;      // 34816
+constexpr int ROPE_BYTES = TILE * 8 * 16;              // 4096
+__device__ __host__ inline int row_rot(int r) { return (r >> 2) & 3; }
+__device__ __host__ inline int main_row_base(int r) { return r * MAIN_ROW_BYTES + row_rot(r) * 16; }
+__device__ __host__ inline int rope_slot(int r, int cr) { return 8 * r + ((cr + (r >> 1)) & 7); }
+
+__device__ inline float wave_max_pair(float v) {
+  // combine lane l with lane l ^ 32
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+
+// Direct-to-LDS 16-byte loads: lane's data lands at M0 + lane * 16.
+// Issued through inline asm so the compiler does not serialise them against
+// unrelated LDS reads; completion is tracked by hand with s_waitcnt vmcnt.
+__device__ inline void dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %0, %1\n\t" ::"v"(voff),
+      "s"(sbase), "s"(lds_base)
+      : "memory", "m0");
+}
+__device__ inline void dma16_vaddr(const void* gptr, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %0, off\n\t" ::"v"(gptr),
+      "s"(lds_base)
+      : "memory", "m0");
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Attention kernel
+// ---------------------------------------------------------------------------
+template <int DQK, int DV, int NHG, typename T>
+__global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
+  constexpr int NSPLIT = 2;              // waves per head group (dims halves)
+  constexpr int NW = NSPLIT * NHG;       // waves per workgroup
+  constexpr int MB = 32 * NHG;           // heads per item (m-block)
+  constexpr int NT = 64 * NW;            // threads
+  constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
+  constexpr int ROWB = DQK * 2;          // bytes per cache row in HBM
+  constexpr int NKS_MAIN = 32 / NSPLIT;  // k-steps over this wave's 512/NSPLIT main dims
+  constexpr int NKS_ROPE = ROPE ? 4 / NSPLIT : 0;  // k-steps over its 64/NSPLIT rope dims
+  constexpr int NKS = NKS_MAIN + NKS_ROPE;
+  constexpr int DVB = DV / 32 / NSPLIT;  // 32-wide dv blocks per wave
+  constexpr int STAGE_BYTES = MAIN_BYTES + (ROPE ? ROPE_BYTES : 0);
+  constexpr int ROWS_PER_WAVE = TILE / NW;            // main-part DMA instructions per wave
+  constexpr int NROPE = ROPE ? TILE / 8 : 0;          // rope DMA instructions per tile
+  static_assert(DQK == 512 || DQK == 576, "head_dim");
+  static_assert(DV == 512, "head_dim_v");
+  static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
+  static_assert(TILE % NW == 0, "rows per wave");
+  typedef MfmaOps<T> Ops;
+
+  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTAGE * STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) f32x4 xchg[NW][4][64];
+  __shared__ uint32_t rowid[RCHUNK];
+  __shared__ uint32_t tmask[RCHUNK / TILE];
+  __shared__ int first_neg;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hg = w % NHG;
+  const int p = w / NHG;
+  const int pw = (NSPLIT - 1 - p) * NHG + hg;  // partner wave (other dims half)
+  const int hlocal = hg * 32 + (lane & 31);  // head within the item's m-block
+  const int hblocks = (a.num_heads + MB - 1) / MB;
+  const int hl = lane >> 5;                // 0: rows {0-3,8-11,..}, 1: rows {4-7,12-15,..}
+  const int my_rope_dma = (w < NROPE) ? ((NROPE - 1 - w) / NW + 1) : 0;
+  // this wave's dims: main chunks [MC p, MC p + MC), rope chunks 64 + [RC p, RC p + RC)
+  // Kᵀ operand: row lane%32, chunk MC p + 2 ks + hl (main) / 64 + RC p + 2 j + hl (rope)
+  constexpr int MC = 64 / NSPLIT, RC = 8 / NSPLIT;
+  const int r_qk = lane & 31;
+  const int qk_base = main_row_base(r_qk) + (MC * p + hl) * 16;
+  int rope_off[NKS_ROPE > 0 ? NKS_ROPE : 1];
+#pragma unroll
+  for (int j = 0; j < NKS_ROPE; ++j) rope_off[j] = MAIN_BYTES + rope_slot(r_qk, RC * p + 2 * j + hl) * 16;
+  // Vᵀ operand (ds_read_b64_tr_b16): 16-lane group (lane>>4) reads rows
+  // 4*hl + (lane&15)/4 (+16q, +8) at dv p*DV/2 + 16*((lane>>4)&1) + 4*(lane&3) (+32d).
+  // Row r+16 has the same rotation as r; row r+8 (r%8 < 4) has rotation +2.
+  const int tr_base = main_row_base(4 * hl + ((lane & 15) >> 2)) + p * (DV / NSPLIT) * 2 +
+                      ((lane >> 4) & 1) * 32 + (lane & 3) * 8;
+
+  // XCD-aware row mapping: consecutive FA rows (pieces of one item) share an XCD.
+  const int nfa = a.num_fa;
+  const int per_xcd = (nfa + 7) >> 3;
+  const int fa_row = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (fa_row >= nfa || (int)(blockIdx.x >> 3) >= per_xcd) return;
+  const int32_t* fa = a.metadata + fa_row * SAS_FA_METADATA_SIZE;
+  if (fa[0] == 0) return;
+  int b = fa[1], m = fa[2];
+  const int j_start = fa[3];
+  const int b_end = fa[4], s_end = fa[5], j_end = fa[6];
+  int slot = fa[7];
+  const int s2b = a.s2_base;
+  const uint32_t kv_base = (uint32_t)(uintptr_t)kv_lds;
+
+  const char* ori_kv = (const char*)a.ori_kv;
+  const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
+  const float sc = a.softmax_scale * LOG2E;
+
+  bool first_item = true;
+  for (;;) {
+    // normalise the cursor: skip batches with no (more) query rows
+    while (b < a.batch && b <= b_end && m >= a.act_q_lens[b] * hblocks) {
+      ++b;
+      m = 0;
+    }
+    if (b >= a.batch || b > b_end || (b == b_end && m > s_end)) break;
+    const bool is_end = (b == b_end && m == s_end);
+    const int s = m / hblocks;
+    const int head = (m - s * hblocks) * MB + hlocal;
+    const bool head_ok = head < a.num_heads;
+    if (is_end && j_end == 0) break;
+
+    const int act_q = a.act_q_lens[b];
+    const int act_kv = a.seqused_kv[b];
+    const int tok = a.q_prefix[b] + s;
+    const ItemGeom g =
+        item_geom(act_q, act_kv, s, a.ori_win_left, a.scenario, a.cmp_ratio, a.topk);
+    const int L = g.n_win + g.n_cmp;
+    const int nblk = (L + s2b - 1) / s2b;
+    const int blo = first_item ? j_start : 0;
+    int bhi = is_end ? j_end : nblk;
+    if (bhi > nblk) bhi = nblk;
+    const bool partial = (first_item && j_start > 0) || is_end;
+    const int p_lo = blo * s2b;
+    const int p_hi = bhi * s2b < L ? bhi * s2b : L;
+    const bool tok_ok = tok >= 0 && tok < a.total_tokens;
+
+    // ---- query fragment for this wave's dims (B operand of Sᵀ = K·Qᵀ) ----
+    i16x8 qf[NKS];
+    {
+      const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
+                                               (head_ok ? head : 0)) * DQK;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int dim = ks < NKS_MAIN ? ((512 / NSPLIT) * p + 16 * ks + 8 * hl)
+                                      : (512 + (64 / NSPLIT) * p + 16 * (ks - NKS_MAIN) + 8 * hl);
+        i16x8 v = *(const i16x8*)(qrow + dim);
+        qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+
+    // ---- online-softmax state (per lane: one head) ----
+    float m_run = partial ? -INFINITY : (head_ok ? a.sinks[head] * LOG2E : -INFINITY);
+    float l_run = partial ? 0.0f : 1.0f;
+    f32x16 acc[DVB];
+#pragma unroll
+    for (int d = 0; d < DVB; ++d)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[d][j] = 0.0f;
+
+    // ---- scenario 3: position of the first -1 among the scanned top-k slots ----
+    const int32_t* idx_row =
+        a.cmp_indices ? a.cmp_indices + (size_t)(tok_ok ? tok : 0) * a.topk : nullptr;
+    int cmp_stop = g.n_cmp;
+    if (a.scenario == 3 && p_hi > g.n_win) {
+      if (tid == 0) first_neg = g.n_cmp;
+      __syncthreads();
+      const int jmax = p_hi - g.n_win;
+      int mine = g.n_cmp;
+      for (int jj = tid; jj < jmax; jj += NT)
+        if (idx_row[jj] == -1 && jj < mine) mine = jj;
+      if (mine < g.n_cmp) atomicMin(&first_neg, mine);
+      __syncthreads();
+      cmp_stop = first_neg;
+    }
+
+    for (int c0 = p_lo; c0 < p_hi; c0 += RCHUNK) {
+      const int clen = (p_hi - c0) < RCHUNK ? (p_hi - c0) : RCHUNK;
+      const int ntile = (clen + TILE - 1) / TILE;
+      // ---- resolve positions -> cache rows (bit 31: compressed cache) ----
+      for (int r = tid; r < ntile * TILE; r += NT) {
+        const int pos = c0 + r;
+        uint32_t id = ROW_INVALID;
+        if (r < clen && tok_ok) {
+          if (pos < g.n_win) {
+            const int lp = g.win_lo + pos;
+            const int bi = lp / a.ori_block_size;
+            if (bi < a.ori_table_len) {
+              const int phys = a.ori_block_table[(size_t)b * a.ori_table_len + bi];
+              if (phys >= 0 && phys < a.ori_block_num)
+                id = (uint32_t)(phys * a.ori_block_size + lp % a.ori_block_size);
+            }
+          } else {
+            const int jj = pos - g.n_win;
+            int cid = -1;
+            if (a.scenario == 2) {
+              cid = jj;
+            } else if (jj < cmp_stop) {
+              const int v = idx_row[jj];
+              if (v >= 0 && v < g.thr) cid = v;
+            }
+            if (cid >= 0) {
+              const int bi = cid / a.cmp_block_size;
+              if (bi < a.cmp_table_len) {
+                const int phys = a.cmp_block_table[(size_t)b * a.cmp_table_len + bi];
+                if (phys >= 0 && phys < a.cmp_block_num)
+                  id = (uint32_t)(phys * a.cmp_block_size + cid % a.cmp_block_size) | 0x80000000u;
+              }
+            }
+          }
+        }
+        rowid[r] = id;
+        const unsigned long long bal = __ballot(id != ROW_INVALID);
+        if (lane == 0) {
+          tmask[(r - lane) / TILE] = (uint32_t)bal;
+          tmask[(r - lane) / TILE + 1] = (uint32_t)(bal >> 32);
+        }
+      }
+      __syncthreads();
+
+      // ---- DMA issue for one tile into one ring stage ----
+      // main part: wave w fills rows w, w + NW, ...; one 1 KB row per instruction
+      // rope part: instruction i fills rows 8i..8i+7 (8 lanes per row)
+      auto row_ptr = [&](uint32_t id) -> const char* {
+        if (id == ROW_INVALID) return ori_kv;  // masked row: any in-bounds address
+        return (id & 0x80000000u) ? cmp_kv + (size_t)(id & 0x7FFFFFFFu) * ROWB
+                                  : ori_kv + (size_t)id * ROWB;
+      };
+      auto issue = [&](int tile, int stage) {
+        const uint32_t sbase = kv_base + stage * STAGE_BYTES;
+#pragma unroll
+        for (int m = 0; m < ROWS_PER_WAVE; ++m) {
+          const int r = w + NW * m;
+          const uint32_t id = __builtin_amdgcn_readfirstlane(rowid[tile * TILE + r]);
+          dma16_sbase(row_ptr(id), (uint32_t)lane * 16u, sbase + main_row_base(r));
+        }
+        if (ROPE) {
+#pragma unroll
+          for (int i0 = 0; i0 < NROPE; i0 += NW) {
+            const int i = i0 + w;
+            if (i < NROPE) {
+              const int r = 8 * i + (lane >> 3);
+              const int cr = ((lane & 7) - (r >> 1)) & 7;
+              const char* src = row_ptr(rowid[tile * TILE + r]) + 1024 + cr * 16;
+              dma16_vaddr(src, sbase + MAIN_BYTES + i * 1024);
+            }
+          }
+        }
+      };
+      // waits until at most the next tile's DMA instructions of this wave are in flight
+      auto wait_tile = [&](bool next_in_flight) {
+        if (!next_in_flight) {
+          wait_vmcnt<0>();
+        } else if (!ROPE || my_rope_dma == 0) {
+          wait_vmcnt<ROWS_PER_WAVE>();
+        } else if (my_rope_dma == 1) {
+          wait_vmcnt<ROWS_PER_WAVE + 1>();
+        } else {
+          wait_vmcnt<ROWS_PER_WAVE + 2>();
+        }
+      };
+
+      issue(0, 0);
+      if (ntile > 1) issue(1, 1);
+
+      for (int it = 0; it < ntile; ++it) {
+        const int stage = it % NSTAGE;
+        wait_tile(it + 1 < ntile);
+        __syncthreads();
+        if (it + 2 < ntile) issue(it + 2, (it + 2) % NSTAGE);
+
+        const unsigned char* sb = kv_lds + stage * STAGE_BYTES;
+        // ---- Sᵀ partial over this wave's dims ----
+        f32x16 st;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) st[j] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const unsigned char* ka;
+          if (ks < NKS_MAIN)
+            ka = sb + qk_base + ks * 32;
+          else
+            ka = sb + rope_off[ks - NKS_MAIN];
+          const i16x8 kop = *(const i16x8*)ka;
+          st = Ops::mma(kop, qf[ks], st);
+          if ((ks & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound operand prefetch
+        }
+        {
+          // ---- sum the two dims halves through LDS ----
+  #pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            xchg[w][q4][lane] = (f32x4){st[4 * q4], st[4 * q4 + 1], st[4 * q4 + 2], st[4 * q4 + 3]};
+          __syncthreads();
+  #pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const f32x4 o = xchg[pw][q4][lane];
+            // identical operand order in both waves -> bitwise identical sums
+            if (p == 0) {
+              st[4 * q4] += o[0]; st[4 * q4 + 1] += o[1]; st[4 * q4 + 2] += o[2]; st[4 * q4 + 3] += o[3];
+            } else {
+              st[4 * q4] = o[0] + st[4 * q4]; st[4 * q4 + 1] = o[1] + st[4 * q4 + 1];
+              st[4 * q4 + 2] = o[2] + st[4 * q4 + 2]; st[4 * q4 + 3] = o[3] + st[4 * q4 + 3];
+            }
+          }
+        }
+
+        // ---- online softmax (exp2 domain), in place on the Sᵀ accumulator ----
+        const uint32_t vm = tmask[it];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int row = 8 * (j >> 2) + 4 * hl + (j & 3);
+          st[j] = ((vm >> row) & 1u) ? st[j] * sc : -INFINITY;
+          mx = fmaxf(mx, st[j]);
+        }
+        mx = wave_max_pair(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const bool need = m_new > m_run + RESCALE_TAU;
+        if (__any(need)) {
+          const float m2 = need ? m_new : m_run;
+          const float alpha = (m2 == m_run) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m2);
+          l_run *= alpha;
+#pragma unroll
+          for (int d = 0; d < DVB; ++d)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
+          m_run = m2;
+        }
+        float psum = 0.0f;
+        i16x8 pk[2];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float pv = (st[j] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(st[j] - m_run);
+          psum += pv;
+          pk[j >> 3][j & 7] = Ops::from_f32(pv);
+        }
+        psum += __shfl_xor(psum, 32);
+        l_run += psum;
+
+        // ---- Oᵀ += Vᵀ · Pᵀ ----
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const i16x8 bop = pk[q];
+#pragma unroll
+          for (int d = 0; d < DVB; ++d) {
+            const unsigned char* pa = sb + tr_base + (16 * q) * MAIN_ROW_BYTES + d * 64;
+            const i16x4 lo4 =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((SAS_LDS i16x4*)(SAS_LDS void*)pa);
+            const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (SAS_LDS i16x4*)(SAS_LDS void*)(pa + 8 * MAIN_ROW_BYTES + 32));  // rot +2
+            const i16x8 aop = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            acc[d] = Ops::mma(aop, bop, acc[d]);
+            if ((d & 1) == 1) __builtin_amdgcn_sched_barrier(0);  // bound operand prefetch
+          }
+        }
+      }
+      __syncthreads();  // rowid / tmask / ring are rewritten by the next chunk or item
+    }
+
+    // ---- epilogue ----
+    if (tok_ok && head_ok) {
+      if (!partial) {
+        T* orow = (T*)a.out + ((size_t)tok * a.num_heads + head) * DV;
+        const float inv = 1.0f / l_run;
+#pragma unroll
+        for (int d = 0; d < DVB; ++d)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int dv = p * (DV / NSPLIT) + 32 * d + 8 * g4 + 4 * hl;
+            const i16x4 v = {Ops::from_f32(acc[d][4 * g4] * inv),
+                             Ops::from_f32(acc[d][4 * g4 + 1] * inv),
+                             Ops::from_f32(acc[d][4 * g4 + 2] * inv),
+                             Ops::from_f32(acc[d][4 * g4 + 3] * inv)};
+            *(i16x4*)(orow + dv) = v;
+          }
+        if (p == 0 && hl == 0) a.lse[(size_t)tok * a.num_heads + head] = (m_run + __log2f(l_run)) * LN2;
+      } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
+        float* wo = a.workspace + ((size_t)slot * MB + hlocal) * DV;
+        const bool empty = !(l_run > 0.0f);
+        const float inv = empty ? 0.0f : 1.0f / l_run;
+#pragma unroll
+        for (int d = 0; d < DVB; ++d)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int dv = p * (DV / NSPLIT) + 32 * d + 8 * g4 + 4 * hl;
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[d][4 * g4 + e] * inv;
+            *(f32x4*)(wo + dv) = v;
+          }
+        if (p == 0 && hl == 0) {
+          float* wl = a.workspace + (size_t)a.num_partial_slots * MB * DV;
+          wl[(size_t)slot * MB + hlocal] =
+              empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
+        }
+      }
+    }
+    if (partial) ++slot;
+    if (is_end) break;
+    first_item = false;
+    ++m;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV merge: lse = log(e^sink + Σ e^lse_i), out = Σ e^(lse_i - lse) o_i
+// ---------------------------------------------------------------------------
+template <int DV, typename T>
+__global__ __launch_bounds__(256) void merge_kernel(const SasAttnArgs a) {
+  const int32_t* fd = a.metadata + SAS_FD_OFFSET + blockIdx.x * SAS_FD_METADATA_SIZE;
+  if (blockIdx.x >= (unsigned)a.num_fd || fd[0] == 0) return;
+  const int mb = a.m_base;
+  const int hblocks = (a.num_heads + mb - 1) / mb;
+  const int b = fd[1], m = fd[2], slot0 = fd[3], npc = fd[4], h0 = fd[5], hn = fd[6];
+  if (b < 0 || b >= a.batch || m < 0 || slot0 < 0 || npc < 1 ||
+      slot0 + npc > a.num_partial_slots || h0 < 0 || hn < 1 || h0 + hn > mb)
+    return;
+  const int s = m / hblocks;
+  const int hbase = (m - s * hblocks) * mb;
+  const int tok = a.q_prefix[b] + s;
+  if (tok < 0 || tok >= a.total_tokens) return;
+  const float* wo = a.workspace;
+  const float* wl = a.workspace + (size_t)a.num_partial_slots * mb * DV;
+  constexpr int V4 = DV / 4;
+  for (int e = threadIdx.x; e < hn * V4; e += blockDim.x) {
+    const int hl = h0 + e / V4;   // head within the m-block
+    const int h = hbase + hl;     // absolute head
+    if (h >= a.num_heads) continue;
+    const int c4 = e % V4;
+    const float sink = a.sinks[h];
+    float mx = sink;
+    for (int i = 0; i < npc; ++i) mx = fmaxf(mx, wl[(size_t)(slot0 + i) * mb + hl]);
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    float lse = -INFINITY;
+    if (mx != -INFINITY) {
+      float tot = expf(sink - mx);
+      for (int i = 0; i < npc; ++i) tot += expf(wl[(size_t)(slot0 + i) * mb + hl] - mx);
+      lse = mx + logf(tot);
+      for (int i = 0; i < npc; ++i) {
+        const float li = wl[(size_t)(slot0 + i) * mb + hl];
+        if (li == -INFINITY) continue;
+        const float wgt = expf(li - lse);
+        const f32x4 v = *(const f32x4*)(wo + ((size_t)(slot0 + i) * mb + hl) * DV + 4 * c4);
+        o[0] += wgt * v[0]; o[1] += wgt * v[1]; o[2] += wgt * v[2]; o[3] += wgt * v[3];
+      }
+    }
+    T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 4 * c4;
+    const i16x4 pk = {MfmaOps<T>::from_f32(o[0]), MfmaOps<T>::from_f32(o[1]),
+                      MfmaOps<T>::from_f32(o[2]), MfmaOps<T>::from_f32(o[3])};
+    *(i16x4*)orow = pk;
+    if (c4 == 0) a.lse[(size_t)tok * a.num_heads + h] = lse;
+  }
+}
+
+template <int DQK, int NHG, typename T>
+static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
+  const int phases = a.phases == 0 ? 3 : a.phases;
+  if (phases & 1) {
+    const int per_xcd = (a.num_fa + 7) / 8;
+    hipLaunchKernelGGL((attn_kernel<DQK, 512, NHG, T>), dim3(8 * per_xcd), dim3(128 * NHG), 0,
+                       st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if ((phases & 2) && a.num_fd > 0) {
+    hipLaunchKernelGGL((merge_kernel<512, T>), dim3(a.num_fd), dim3(256), 0, st, a);
+    return hipGetLastError();
+  }
+  return hipSuccess;
+}
+
+// Items carry m_base = 32 or 64 heads (one or two 32-head groups, each a
+// dims-split wave pair): 2 or 4 waves, one wave per SIMD.
+template <typename T>
+static hipError_t dispatch_heads(const SasAttnArgs& a, hipStream_t st) {
+  if (a.head_dim == 576)
+    return a.m_base == 32 ? launch_attn<576, 1, T>(a, st) : launch_attn<576, 2, T>(a, st);
+  return a.m_base == 32 ? launch_attn<512, 1, T>(a, st) : launch_attn<512, 2, T>(a, st);
+}
+
+}  // namespace sas
+
+extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
+  using sas::set_error;
+  if (!a) {
+    set_error("sas_attention_launch: null args");
+    return SAS_E_INVALID;
+  }
+  if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_q_lens ||
+      !a->seqused_kv || !a->sinks || !a->metadata || !a->out || !a->lse) {
+    set_error("sas_attention_launch: null tensor pointer");
+    return SAS_E_INVALID;
+  }
+  if (a->head_dim != 512 && a->head_dim != 576) {
+    set_error("sas_attention_launch: head_dim must be 512 or 576");
+    return SAS_E_UNSUPPORTED;
+  }
+  if (a->head_dim_v != 512) {
+    set_error("sas_attention_launch: head_dim_v must be 512");
+    return SAS_E_UNSUPPORTED;
+  }
+  if (a->num_heads < 1 || a->num_heads > 128 || (a->num_heads % 16) != 0) {
+    set_error("sas_attention_launch: num_heads must be a multiple of 16 in [16, 128]");
+    return SAS_E_UNSUPPORTED;
+  }
+  if ((a->m_base != 32 && a->m_base != 64) || (a->num_heads <= 32 && a->m_base != 32) ||
+      (a->num_heads > 32 && a->m_base != 64)) {
+    set_error("sas_attention_launch: m_base must be 32 for <= 32 heads, else 64");
+    return SAS_E_INVALID;
+  }
+  if (a->scenario < 1 || a->scenario > 3 || (a->scenario >= 2 && (!a->cmp_kv ||
+      !a->cmp_block_table || a->cmp_ratio < 1)) || (a->scenario == 3 && (!a->cmp_indices ||
+      a->topk < 0))) {
+    set_error("sas_attention_launch: scenario inputs missing");
+    return SAS_E_INVALID;
+  }
+  if (a->phases < 0 || a->phases > 3) {
+    set_error("sas_attention_launch: phases must be 0..3");
+    return SAS_E_INVALID;
+  }
+  if (a->num_fa < 1 || a->num_fa > SAS_AIC_CORE_NUM || a->num_fd < 0 ||
+      a->num_fd > SAS_AIV_CORE_NUM || a->s2_base < 32 || (a->s2_base % 32) != 0 ||
+      (a->num_fd > 0 && (!a->workspace || a->num_partial_slots < 1))) {
+    set_error("sas_attention_launch: inconsistent schedule");
+    return SAS_E_INVALID;
+  }
+  if (a->ori_block_num < 1 || a->ori_block_size < 1 || a->ori_table_len < 1 || a->batch < 0 ||
+      a->total_tokens < 0 || (a->scenario >= 2 && (a->cmp_block_num < 1 ||
+      a->cmp_block_size < 1 || a->cmp_table_len < 1))) {
+    set_error("sas_attention_launch: bad cache geometry");
+    return SAS_E_INVALID;
+  }
+  if ((int64_t)a->ori_block_num * a->ori_block_size >= (1ll << 31) ||
+      (int64_t)a->cmp_block_num * a->cmp_block_size >= (1ll << 31)) {
+    set_error("sas_attention_launch: more than 2^31 cache rows");
+    return SAS_E_UNSUPPORTED;
+  }
+  if (a->batch == 0 || a->total_tokens == 0) return SAS_OK;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = a->dtype == SAS_DTYPE_FP16 ? sas::dispatch_heads<_Float16>(*a, st)
+                                            : sas::dispatch_heads<__bf16>(*a, st);
+  if (e != hipSuccess) {
+    set_error(std::string("sas_attention_launch: ") + hipGetErrorString(e));
+    return SAS_E_HIP;
+  }
+  return SAS_OK;
+}
+
+extern "C" int sas_version(void) { return 100; }
+
+extern "C" int sas_args_struct_size(void) { return (int)sizeof(SasAttnArgs); }
+
+extern "C" const char* sas_last_error(void) { return sas::g_last_error.c_str(); }

@@ -1,0 +1,181 @@
+"""Split-KV scheduler: ``sparse_attn_sharedkv_metadata`` (signature of metadata.py:1018-1045).
+
+The reference ports the AICPU ``SparseAttnSharedkvMetadata`` scheduler to
+Python and its kernel ignores the result (kernel.py:367, "unused, v1"). Here
+the scheduler is C++ inside ``libsas_mi355x.so`` (``sas_metadata_build``) and
+the attention kernel is driven by it: one FA row per workgroup, FD rows for
+the split-KV merges. Row schemas keep metadata.py's field order
+(:45-60); capacities are sized for MI355X (256 CUs, up to 512 workgroups).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import (AIC_CORE_NUM, AIV_CORE_NUM, CFG_OFFSET, FA_METADATA_SIZE,  # noqa: F401
+                   FD_METADATA_SIZE, FD_OFFSET, META_MAGIC, SAS_META_SIZE)
+
+# Field indices (metadata.py:45-60)
+FA_CORE_ENABLE_INDEX = 0
+FA_BN2_START_INDEX = 1
+FA_M_START_INDEX = 2
+FA_S2_START_INDEX = 3
+FA_BN2_END_INDEX = 4
+FA_M_END_INDEX = 5
+FA_S2_END_INDEX = 6
+FA_FIRST_FD_DATA_WORKSPACE_IDX_INDEX = 7
+
+FD_CORE_ENABLE_INDEX = 0
+FD_BN2_IDX_INDEX = 1
+FD_M_IDX_INDEX = 2
+FD_WORKSPACE_IDX_INDEX = 3
+FD_WORKSPACE_NUM_INDEX = 4
+FD_M_START_INDEX = 5
+FD_M_NUM_INDEX = 6
+
+# MI355X: 256 compute units; one attention workgroup per CU.
+DEFAULT_CORE_NUM = 256
+DEFAULT_S2_BASE = 64          # positions per schedulable block
+DEFAULT_MIN_SPLIT_BLOCKS = 2  # never split an item into pieces shorter than 128 positions
+DEFAULT_FD_HEAD_CHUNK = 32    # heads per merge task
+
+
+def m_base_for(num_heads: int) -> int:
+    """Heads per schedulable item (the reference's mBaseSize): 32 or 64."""
+    return 32 if num_heads <= 32 else 64
+
+
+def _as_list(t) -> List[int]:
+    if t is None:
+        return []
+    if isinstance(t, torch.Tensor):
+        return [int(x) for x in t.detach().cpu().to(torch.int64).tolist()]
+    return [int(x) for x in t]
+
+
+def resolve_lengths(*, layout_q: str, layout_kv: str, cu_seqlens_q=None, cu_seqlens_ori_kv=None,
+                    seqused_q=None, seqused_kv=None, batch_size: int = 0, max_seqlen_q: int = 0,
+                    max_seqlen_kv: int = 0):
+    """Per-batch (act_q, act_kv) the way metadata.py:345-407 derives them."""
+    cu_q, cu_kv = _as_list(cu_seqlens_q), _as_list(cu_seqlens_ori_kv)
+    sq, skv = _as_list(seqused_q), _as_list(seqused_kv)
+    if sq:
+        batch = len(sq)
+    elif layout_q == "TND" and cu_q:
+        batch = len(cu_q) - 1
+    else:
+        batch = int(batch_size)
+    act_q, act_kv = [], []
+    for b in range(batch):
+        if sq:
+            act_q.append(sq[b])
+        elif layout_q == "TND" and cu_q:
+            act_q.append(cu_q[b + 1] - cu_q[b])
+        else:
+            act_q.append(int(max_seqlen_q))
+        if skv:
+            act_kv.append(skv[b])
+        elif layout_kv == "TND" and cu_kv:
+            act_kv.append(cu_kv[b + 1] - cu_kv[b])
+        else:
+            act_kv.append(int(max_seqlen_kv))
+    return act_q, act_kv
+
+
+def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: int,
+                   ori_win_left: int, scenario: int, cmp_ratio: int, cmp_topk: int,
+                   core_num: int = DEFAULT_CORE_NUM, s2_base: int = DEFAULT_S2_BASE,
+                   min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
+                   fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK) -> torch.Tensor:
+    """Run the C++ scheduler; returns an int32 CPU tensor of ``SAS_META_SIZE`` words."""
+    lib = _lib.load()
+    b = len(act_q)
+    out = torch.zeros(SAS_META_SIZE, dtype=torch.int32)
+    aq = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_q])
+    ak = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_kv])
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    rc = lib.sas_metadata_build(ctypes.cast(out.data_ptr(), i32p), b, aq, ak, int(num_heads),
+                                m_base_for(int(num_heads)), int(ori_win_left), int(scenario),
+                                int(cmp_ratio), int(cmp_topk), int(core_num), int(s2_base),
+                                int(min_split_blocks), int(fd_head_chunk))
+    if rc < 0:
+        raise ValueError(_lib.last_error())
+    return out
+
+
+def config_row(metadata: torch.Tensor) -> dict:
+    """Decode the schedule summary row (host copy; syncs if ``metadata`` is on a GPU)."""
+    cfg = metadata.reshape(-1)[CFG_OFFSET:CFG_OFFSET + 8].to("cpu").tolist()
+    if cfg[0] != META_MAGIC:
+        raise AssertionError("metadata was not produced by sparse_attn_sharedkv_metadata")
+    return dict(s2_base=cfg[1], num_fa=cfg[2], num_fd=cfg[3], num_partial_slots=cfg[4],
+                num_heads=cfg[5], m_base=cfg[6], total_items=cfg[7])
+
+
+def sparse_attn_sharedkv_metadata(
+    *,
+    num_heads_q: int,
+    num_heads_kv: int,
+    head_dim: int,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    cu_seqlens_ori_kv: Optional[torch.Tensor] = None,
+    cu_seqlens_cmp_kv: Optional[torch.Tensor] = None,
+    seqused_q: Optional[torch.Tensor] = None,
+    seqused_kv: Optional[torch.Tensor] = None,
+    batch_size: int = 0,
+    max_seqlen_q: int = 0,
+    max_seqlen_kv: int = 0,
+    ori_topk: int = 0,
+    cmp_topk: int = 0,
+    cmp_ratio: int = -1,
+    ori_mask_mode: int = 4,
+    cmp_mask_mode: int = 3,
+    ori_win_left: int = 127,
+    ori_win_right: int = 0,
+    layout_q: str = "BSND",
+    layout_kv: str = "PA_ND",
+    has_ori_kv: bool = True,
+    has_cmp_kv: bool = True,
+    aic_core_num: int = DEFAULT_CORE_NUM,
+    aiv_core_num: int = 2 * DEFAULT_CORE_NUM,
+    device: Optional[str] = None,
+) -> torch.Tensor:
+    """Schedule for one ``sparse_attn_sharedkv`` call: int32 ``[SAS_META_SIZE]``.
+
+    Scenario: ``has_cmp_kv`` with ``cmp_topk > 0`` is top-k compressed (SCFA),
+    ``has_cmp_kv`` alone is dense compressed (CFA), otherwise sliding window
+    (SWA) -- the same rule as metadata.py:382-386. ``ori_win_left = -1`` is
+    an empty raw window (golden.py:128-131 semantics, used for pure top-k
+    decode). ``aic_core_num`` is the number of workgroups to balance over.
+    ``aiv_core_num``, ``head_dim`` and ``ori_topk`` are accepted for signature
+    parity; merge tasks are bounded by ``AIV_CORE_NUM``.
+    """
+    del cu_seqlens_cmp_kv, head_dim, ori_topk, aiv_core_num
+    if num_heads_kv != 1:
+        raise ValueError(f"only num_heads_kv=1 (shared KV) is supported, got {num_heads_kv}")
+    if ori_mask_mode != 4 or ori_win_right != 0:
+        raise ValueError("only ori_mask_mode=4 with ori_win_right=0 is supported")
+    if has_cmp_kv and cmp_mask_mode != 3:
+        raise ValueError("only cmp_mask_mode=3 is supported")
+    if not has_ori_kv:
+        raise ValueError("has_ori_kv=False is not supported")
+    if has_cmp_kv:
+        scenario = 3 if cmp_topk > 0 else 2
+        if cmp_ratio < 1:
+            raise ValueError("cmp_ratio must be >= 1 when a compressed cache is present")
+    else:
+        scenario = 1
+    act_q, act_kv = resolve_lengths(layout_q=layout_q, layout_kv=layout_kv,
+                                    cu_seqlens_q=cu_seqlens_q,
+                                    cu_seqlens_ori_kv=cu_seqlens_ori_kv, seqused_q=seqused_q,
+                                    seqused_kv=seqused_kv, batch_size=batch_size,
+                                    max_seqlen_q=max_seqlen_q, max_seqlen_kv=max_seqlen_kv)
+    md = build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads_q,
+                        ori_win_left=ori_win_left, scenario=scenario,
+                        cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
+                        core_num=min(int(aic_core_num), AIC_CORE_NUM))
+    return md.to(device) if device is not None else md

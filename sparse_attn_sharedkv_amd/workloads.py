@@ -1,0 +1,146 @@
+"""Synthetic benchmark workloads, generated directly on the GPU.
+
+Shapes (BSND, block_size 64, q and KV ~ N(0, 1) * 0.5, softmax_scale = 1/sqrt(d_qk)):
+
+* ``topk_decode_b2_h16_k256``        B=2, H=16, ctx 1024, top-k 256, no sink
+* ``swa_decode_b32_h64``             B=32, H=64, ctx U[2048, 8192], window 128, sinks U(-1,1)
+* ``swa_topk_decode_b32_h64_k512``   B=32, H=64, ctx 16384, window 128 + compressed
+                                     (ratio 4) top-k 512, sinks U(-1,1)
+* ``mla_decode_b64_h128_k2048``      DeepSeek-V3.2 sparse MLA decode: B=64, H=128,
+                                     ctx 32768, top-k 2048, no sink
+* ``mla_mtp_decode_b64_h128_k2048``  the same with two query rows per sequence (MTP)
+
+d_qk = 576 (512 latent + 64 rope), d_v = 512 throughout. Pure top-k attention
+is expressed through the reference API as a compressed cache equal to the raw
+pool with cmp_ratio 1 and an empty raw window (ori_win_left = -1). Block
+tables hand each sequence a random permutation slice of the pool; top-k rows
+are ``randperm(thr)[:K]`` per query row, ``-1`` padded (the generators of the
+reference's golden.py:315-473, on the device). One generator per tensor
+(q 0, kv 1, tables 2, indices 3, lengths 4, sinks 5).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Sequence
+
+import numpy as np
+import torch
+
+WORKLOADS: Dict[str, dict] = {
+    "topk_decode_b2_h16_k256": dict(B=2, S=1, H=16, D=576, DV=512, ctx=(1024, 1024), K=256,
+                                    window=-1, cmp_ratio=1, mode="topk", sinks="none"),
+    "swa_decode_b32_h64": dict(B=32, S=1, H=64, D=576, DV=512, ctx=(2048, 8192), K=0,
+                               window=127, cmp_ratio=None, mode="swa", sinks="uniform"),
+    "swa_topk_decode_b32_h64_k512": dict(B=32, S=1, H=64, D=576, DV=512, ctx=(16384, 16384),
+                                         K=512, window=127, cmp_ratio=4, mode="swa+topk",
+                                         sinks="uniform"),
+    "mla_decode_b64_h128_k2048": dict(B=64, S=1, H=128, D=576, DV=512, ctx=(32768, 32768),
+                                      K=2048, window=-1, cmp_ratio=1, mode="topk", sinks="none"),
+    "mla_mtp_decode_b64_h128_k2048": dict(B=64, S=2, H=128, D=576, DV=512, ctx=(32768, 32768),
+                                          K=2048, window=-1, cmp_ratio=1, mode="topk",
+                                          sinks="none"),
+}
+
+
+def _pool(lens, block_size, d, dtype, rng, gen, device):
+    per_b = [math.ceil(x / block_size) for x in lens]
+    nblk = max(sum(per_b), 1)
+    phys = rng.permutation(nblk).astype(np.int32)
+    table = np.full((len(lens), max(max(per_b), 1)), -1, dtype=np.int32)
+    cur = 0
+    for b, nb in enumerate(per_b):
+        table[b, :nb] = phys[cur:cur + nb]
+        cur += nb
+    pool = (torch.randn((nblk, block_size, 1, d), generator=gen, device=device) * 0.5).to(dtype)
+    return pool, torch.as_tensor(table, dtype=torch.int32, device=device)
+
+
+def build_workload(name: str, *, device="cuda", seed: int = 0, batch: Optional[int] = None,
+                   ctx_override: Optional[Sequence[int]] = None, block_size: int = 64,
+                   dtype=torch.bfloat16) -> dict:
+    """Keyword arguments of ``sparse_flash_mla`` for one input set (plus ``head_dim_v``)."""
+    w = WORKLOADS[name]
+    b = int(batch if batch is not None else w["B"])
+    s_q, h, d, dv, k = w["S"], w["H"], w["D"], w["DV"], w["K"]
+    dev = torch.device(device)
+
+    def gen(i):
+        return torch.Generator(device=dev).manual_seed(seed * 16 + i)
+
+    if ctx_override is not None:
+        lens = [int(x) for x in ctx_override]
+        b = len(lens)
+    else:
+        lo, hi = w["ctx"]
+        lg = torch.Generator().manual_seed(seed * 16 + 4)
+        lens = [lo if lo == hi else int(x) for x in
+                torch.randint(lo, hi + 1, (b,), generator=lg).tolist()]
+    q = (torch.randn((b, s_q, h, d), generator=gen(0), device=dev) * 0.5).to(dtype)
+    kvg = gen(1)
+    rng = np.random.default_rng(seed * 16 + 2)
+    ori_kv, ori_bt = _pool(lens, block_size, d, dtype, rng, kvg, dev)
+    cmp_kv = cmp_bt = None
+    if w["mode"] == "topk":
+        cmp_kv, cmp_bt = ori_kv, ori_bt
+    elif w["mode"] == "swa+topk":
+        cmp_kv, cmp_bt = _pool([x // w["cmp_ratio"] for x in lens], block_size, d, dtype, rng,
+                               kvg, dev)
+    idx = None
+    if k > 0:
+        ig = gen(3)
+        idx = torch.full((b * s_q, k), -1, dtype=torch.int32, device=dev)
+        for bi in range(b):
+            for s in range(s_q):
+                thr = max(0, (lens[bi] - s_q + s + 1) // w["cmp_ratio"])
+                if thr:
+                    perm = torch.randperm(thr, generator=ig, device=dev)[:k].to(torch.int32)
+                    idx[bi * s_q + s, :perm.numel()] = perm
+        idx = idx.reshape(b, s_q, 1, k)
+    if w["sinks"] == "none":
+        sinks = torch.full((h,), float("-inf"), dtype=torch.float32, device=dev)
+    else:
+        sinks = (torch.rand((h,), generator=gen(5), device=dev) * 2 - 1).to(torch.float32)
+    return dict(q=q, ori_kv=ori_kv, ori_block_table=ori_bt, cmp_kv=cmp_kv,
+                cmp_block_table=cmp_bt, cmp_sparse_indices=idx,
+                seqused_kv=torch.tensor(lens, dtype=torch.int32, device=dev), sinks=sinks,
+                softmax_scale=1.0 / math.sqrt(d), cmp_ratio=w["cmp_ratio"],
+                ori_win_left=w["window"], layout_q="BSND", head_dim_v=dv,
+                topk_cmp=k if k > 0 else None)
+
+
+def workload_counts(args: dict) -> dict:
+    """Query tokens, attended rows and top-k width of one input set."""
+    q = args["q"]
+    b, s_q, h, d = q.shape
+    dv = args.get("head_dim_v") or d
+    lens = [int(x) for x in args["seqused_kv"].cpu().tolist()]
+    win = args["ori_win_left"]
+    idx = args["cmp_sparse_indices"]
+    valid = None
+    if idx is not None:
+        valid = (idx.reshape(b * s_q, -1) >= 0).sum(dim=1).cpu().tolist()
+    rows = 0
+    for bi in range(b):
+        for s in range(s_q):
+            sg = lens[bi] - s_q + s
+            rows += max(0, sg + 1 - max(sg - win, 0))
+            if valid is not None:
+                rows += int(valid[bi * s_q + s])
+    return dict(tokens=b * s_q, rows=rows, heads=h, d_qk=d, d_v=dv,
+                k=idx.shape[-1] if idx is not None else 0)
+
+
+def flops_and_bytes(counts: dict, kv_row_bytes: Optional[int] = None) -> tuple:
+    """Algorithmic FLOPs and HBM bytes of one call.
+
+    FLOPs = 2 * rows * H * (d_qk + d_v). Bytes = gathered rows (once per query
+    token, shared by all heads) + q + out + lse + top-k indices + one block-table
+    entry per gathered row.
+    """
+    t, rows, h = counts["tokens"], counts["rows"], counts["heads"]
+    dq, dv, k = counts["d_qk"], counts["d_v"], counts["k"]
+    rb = kv_row_bytes if kv_row_bytes is not None else dq * 2
+    flops = 2.0 * rows * h * (dq + dv)
+    nbytes = rows * rb + t * h * dq * 2 + t * h * dv * 2 + t * h * 4 + t * k * 4 + rows * 4
+    return flops, float(nbytes)

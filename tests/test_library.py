@@ -1,0 +1,62 @@
+"""The C-ABI library loads on a CPU-only host and exports what the header declares.
+
+No compute calls are made here (there is no GPU); host-side entry points
+(the scheduler, the workspace size, the argument-struct layout) are called.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from sparse_attn_sharedkv_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sas_mi355x.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sas_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared_functions()
+    assert names, "no declarations parsed"
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in sas_mi355x.h but not exported"
+    assert set(names) == set(_lib.EXPORTS)
+
+
+def test_struct_layout_matches_binding():
+    lib = _lib.load()
+    assert lib.sas_args_struct_size() == ctypes.sizeof(_lib.SasAttnArgs)
+    assert lib.sas_version() >= 100
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (SAS_[A-Z_]+) (\S+)", text))
+    assert int(consts["SAS_AIC_CORE_NUM"]) == _lib.AIC_CORE_NUM
+    assert int(consts["SAS_AIV_CORE_NUM"]) == _lib.AIV_CORE_NUM
+    assert int(consts["SAS_META_SIZE"]) == _lib.SAS_META_SIZE
+    assert int(consts["SAS_META_MAGIC"], 16) == _lib.META_MAGIC
+
+
+def test_workspace_bytes():
+    lib = _lib.load()
+    assert lib.sas_workspace_bytes(256, 64, 512) == 256 * 64 * 513 * 4
+    assert lib.sas_workspace_bytes(-1, 64, 512) == 0
+
+
+def test_launch_rejects_bad_arguments_without_a_gpu():
+    # argument validation runs before any HIP call
+    lib = _lib.load()
+    a = _lib.SasAttnArgs()
+    assert lib.sas_attention_launch(None, None) == -1
+    assert lib.sas_attention_launch(ctypes.byref(a), None) == -1
+    assert "null" in _lib.last_error()
