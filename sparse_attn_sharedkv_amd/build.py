@@ -21,6 +21,10 @@ HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     # packed FP32 VALU forms are kept out of generated code on this target
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the online-softmax rescale multiplies them with
+    # VALU ops, which cannot read AGPRs (AGPR-resident accumulators cost a full
+    # copy out and back on every tile)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"),
 ]
 

@@ -121,19 +121,40 @@ __device__ inline void dma16_sbase(const void* sbase, uint32_t voff, uint32_t ld
       "s_mov_b32 m0, %2\n\t"
       "global_load_lds_dwordx4 %0, %1\n\t" ::"v"(voff),
       "s"(sbase), "s"(lds_base)
-      : "memory", "m0");
+      : "memory");
 }
 __device__ inline void dma16_vaddr(const void* gptr, uint32_t lds_base) {
   asm volatile(
       "s_mov_b32 m0, %1\n\t"
       "global_load_lds_dwordx4 %0, off\n\t" ::"v"(gptr),
       "s"(lds_base)
-      : "memory", "m0");
+      : "memory");
 }
 
 template <int N>
 __device__ inline void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// ds_read_b64_tr_b16 with an immediate offset (the builtin does not fold
+// offsets, which costs one address VGPR per read). The result is not tracked
+// by the compiler's lgkmcnt bookkeeping: consume it only after lds_wait_group.
+template <int OFF>
+__device__ inline i16x4 ds_read_tr16(uint32_t addr) {
+  i16x4 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+  return v;
+}
+
+// Wait until at most N LDS operations are outstanding; the eight registers
+// pass through the asm so no consumer can be scheduled above the wait.
+template <int N>
+__device__ inline void lds_wait_group(i16x4 (&r)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                 "+v"(r[6]), "+v"(r[7])
+               : "n"(N)
+               : "memory");
 }
 
 // ---------------------------------------------------------------------------
@@ -237,20 +258,9 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
     const int p_hi = bhi * s2b < L ? bhi * s2b : L;
     const bool tok_ok = tok >= 0 && tok < a.total_tokens;
 
-    // ---- query fragment for this wave's dims (B operand of Sᵀ = K·Qᵀ) ----
+    // query fragment for this wave's dims (B operand of Sᵀ = K·Qᵀ); loaded once
+    // per item, after the first gathers are in flight
     i16x8 qf[NKS];
-    {
-      const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
-                                               (head_ok ? head : 0)) * DQK;
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const int dim = ks < NKS_MAIN ? ((512 / NSPLIT) * p + 16 * ks + 8 * hl)
-                                      : (512 + (64 / NSPLIT) * p + 16 * (ks - NKS_MAIN) + 8 * hl);
-        i16x8 v = *(const i16x8*)(qrow + dim);
-        qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-
     // ---- online-softmax state (per lane: one head) ----
     float m_run = partial ? -INFINITY : (head_ok ? a.sinks[head] * LOG2E : -INFINITY);
     float l_run = partial ? 0.0f : 1.0f;
@@ -261,16 +271,30 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
       for (int j = 0; j < 16; ++j) acc[d][j] = 0.0f;
 
     // ---- scenario 3: position of the first -1 among the scanned top-k slots ----
+    // (golden.py:48-53: the scan stops at the first -1). Loads are batched:
+    // every thread issues its SCAN_PER loads before testing any of them.
     const int32_t* idx_row =
         a.cmp_indices ? a.cmp_indices + (size_t)(tok_ok ? tok : 0) * a.topk : nullptr;
     int cmp_stop = g.n_cmp;
     if (a.scenario == 3 && p_hi > g.n_win) {
       if (tid == 0) first_neg = g.n_cmp;
       __syncthreads();
-      const int jmax = p_hi - g.n_win;
+      const int jmax = min(p_hi - g.n_win, g.n_cmp);
+      constexpr int SCAN_PER = 8;
       int mine = g.n_cmp;
-      for (int jj = tid; jj < jmax; jj += NT)
-        if (idx_row[jj] == -1 && jj < mine) mine = jj;
+      for (int j0 = 0; j0 < jmax; j0 += NT * SCAN_PER) {
+        int v[SCAN_PER];
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) {  // unconditional, clamped: all loads in flight at once
+          const int jj = j0 + e * NT + tid;
+          v[e] = idx_row[jj < jmax ? jj : jmax - 1];
+        }
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) {
+          const int jj = j0 + e * NT + tid;
+          if (jj < jmax && v[e] == -1 && jj < mine) mine = jj;
+        }
+      }
       if (mine < g.n_cmp) atomicMin(&first_neg, mine);
       __syncthreads();
       cmp_stop = first_neg;
@@ -280,35 +304,50 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
       const int clen = (p_hi - c0) < RCHUNK ? (p_hi - c0) : RCHUNK;
       const int ntile = (clen + TILE - 1) / TILE;
       // ---- resolve positions -> cache rows (bit 31: compressed cache) ----
-      for (int r = tid; r < ntile * TILE; r += NT) {
+      // Thread tid owns positions c0 + e*NT + tid. Phase 1 issues the top-k
+      // loads, phase 2 the block-table loads, phase 3 packs and publishes.
+      constexpr int PER = RCHUNK / NT;
+      int cid[PER];
+      int tab[PER];  // block-table word to read, or -1
+      // Loads are unconditional with clamped, always in-bounds indices (so all
+      // of a phase's loads are in flight together); results are masked after.
+      const bool scan3 = a.scenario == 3 && idx_row != nullptr && a.topk > 0;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int r = e * NT + tid;
+        const int pos = c0 + r;
+        const int jj = pos - g.n_win;
+        int v = jj;
+        if (scan3) v = idx_row[jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1)];
+        const bool live = r < clen && tok_ok && pos >= g.n_win && (a.scenario == 2 || jj < cmp_stop);
+        cid[e] = live ? v : -1;
+      }
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int r = e * NT + tid;
+        const int pos = c0 + r;
+        const bool win = pos < g.n_win;
+        const int key = win ? g.win_lo + pos : cid[e];
+        const int bsz = win ? a.ori_block_size : a.cmp_block_size;
+        const int tlen = win ? a.ori_table_len : a.cmp_table_len;
+        const int32_t* tbl = win ? a.ori_block_table : a.cmp_block_table;
+        const int bi = key >= 0 ? key / bsz : 0;
+        const bool ok = r < clen && tok_ok && key >= 0 && bi < tlen && (win || cid[e] < g.thr);
+        const int t = (tbl != nullptr) ? tbl[(size_t)b * tlen + (bi < tlen ? bi : tlen - 1)] : -1;
+        tab[e] = ok ? t : -1;
+      }
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int r = e * NT + tid;
         const int pos = c0 + r;
         uint32_t id = ROW_INVALID;
-        if (r < clen && tok_ok) {
+        const int phys = tab[e];
+        if (r < clen && tok_ok && phys >= 0) {
           if (pos < g.n_win) {
-            const int lp = g.win_lo + pos;
-            const int bi = lp / a.ori_block_size;
-            if (bi < a.ori_table_len) {
-              const int phys = a.ori_block_table[(size_t)b * a.ori_table_len + bi];
-              if (phys >= 0 && phys < a.ori_block_num)
-                id = (uint32_t)(phys * a.ori_block_size + lp % a.ori_block_size);
-            }
-          } else {
-            const int jj = pos - g.n_win;
-            int cid = -1;
-            if (a.scenario == 2) {
-              cid = jj;
-            } else if (jj < cmp_stop) {
-              const int v = idx_row[jj];
-              if (v >= 0 && v < g.thr) cid = v;
-            }
-            if (cid >= 0) {
-              const int bi = cid / a.cmp_block_size;
-              if (bi < a.cmp_table_len) {
-                const int phys = a.cmp_block_table[(size_t)b * a.cmp_table_len + bi];
-                if (phys >= 0 && phys < a.cmp_block_num)
-                  id = (uint32_t)(phys * a.cmp_block_size + cid % a.cmp_block_size) | 0x80000000u;
-              }
-            }
+            if (phys < a.ori_block_num)
+              id = (uint32_t)(phys * a.ori_block_size + (g.win_lo + pos) % a.ori_block_size);
+          } else if (phys < a.cmp_block_num) {
+            id = (uint32_t)(phys * a.cmp_block_size + cid[e] % a.cmp_block_size) | 0x80000000u;
           }
         }
         rowid[r] = id;
@@ -330,10 +369,12 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
       };
       auto issue = [&](int tile, int stage) {
         const uint32_t sbase = kv_base + stage * STAGE_BYTES;
+        // lane m holds the row id of this wave's m-th row of the tile
+        const uint32_t my_ids = rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)];
 #pragma unroll
         for (int m = 0; m < ROWS_PER_WAVE; ++m) {
           const int r = w + NW * m;
-          const uint32_t id = __builtin_amdgcn_readfirstlane(rowid[tile * TILE + r]);
+          const uint32_t id = __builtin_amdgcn_readlane(my_ids, m);
           dma16_sbase(row_ptr(id), (uint32_t)lane * 16u, sbase + main_row_base(r));
         }
         if (ROPE) {
@@ -364,6 +405,21 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
 
       issue(0, 0);
       if (ntile > 1) issue(1, 1);
+      if (c0 == p_lo) {
+        const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
+                                                 (head_ok ? head : 0)) * DQK;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const int dim = ks < NKS_MAIN ? ((512 / NSPLIT) * p + 16 * ks + 8 * hl)
+                                        : (512 + (64 / NSPLIT) * p + 16 * (ks - NKS_MAIN) + 8 * hl);
+          i16x8 v = *(const i16x8*)(qrow + dim);
+          qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        // A wait the compiler can see: it clears its pending-load state here, so it
+        // puts no vmcnt wait for qf inside the tile loop (that wait would also drain
+        // the row DMAs in flight on every tile). Also lands tiles 0 and 1.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+      }
 
       for (int it = 0; it < ntile; ++it) {
         const int stage = it % NSTAGE;
@@ -372,20 +428,25 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
         if (it + 2 < ntile) issue(it + 2, (it + 2) % NSTAGE);
 
         const unsigned char* sb = kv_lds + stage * STAGE_BYTES;
-        // ---- Sᵀ partial over this wave's dims ----
+        // ---- Sᵀ partial over this wave's dims (K operands prefetched 3 deep) ----
         f32x16 st;
 #pragma unroll
         for (int j = 0; j < 16; ++j) st[j] = 0.0f;
+        {
+          auto kaddr = [&](int ks) -> const i16x8* {
+            return (const i16x8*)(ks < NKS_MAIN ? sb + qk_base + ks * 32
+                                                : sb + rope_off[ks - NKS_MAIN]);
+          };
+          constexpr int PF = 3;
+          i16x8 kbuf[PF];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const unsigned char* ka;
-          if (ks < NKS_MAIN)
-            ka = sb + qk_base + ks * 32;
-          else
-            ka = sb + rope_off[ks - NKS_MAIN];
-          const i16x8 kop = *(const i16x8*)ka;
-          st = Ops::mma(kop, qf[ks], st);
-          if ((ks & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound operand prefetch
+          for (int i = 0; i < PF; ++i) kbuf[i] = *kaddr(i);
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            const i16x8 kop = kbuf[ks % PF];
+            if (ks + PF < NKS) kbuf[ks % PF] = *kaddr(ks + PF);
+            st = Ops::mma(kop, qf[ks], st);
+          }
         }
         {
           // ---- sum the two dims halves through LDS ----
@@ -439,21 +500,55 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
         psum += __shfl_xor(psum, 32);
         l_run += psum;
 
-        // ---- Oᵀ += Vᵀ · Pᵀ ----
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const i16x8 bop = pk[q];
-#pragma unroll
-          for (int d = 0; d < DVB; ++d) {
-            const unsigned char* pa = sb + tr_base + (16 * q) * MAIN_ROW_BYTES + d * 64;
-            const i16x4 lo4 =
-                __builtin_amdgcn_ds_read_tr16_b64_v4i16((SAS_LDS i16x4*)(SAS_LDS void*)pa);
-            const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (SAS_LDS i16x4*)(SAS_LDS void*)(pa + 8 * MAIN_ROW_BYTES + 32));  // rot +2
-            const i16x8 aop = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-            acc[d] = Ops::mma(aop, bop, acc[d]);
-            if ((d & 1) == 1) __builtin_amdgcn_sched_barrier(0);  // bound operand prefetch
+        // ---- Oᵀ += Vᵀ · Pᵀ: groups of 4 dv blocks (8 transposed reads), double-buffered ----
+        {
+          static_assert(DVB % 4 == 0, "dv blocks come in groups of 4");
+          constexpr int NG = 2 * DVB / 4;  // groups: (q, d0..d0+3)
+          const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
+          i16x4 gbuf[2][8];
+#define SAS_TR_GROUP(GI, DST)                                                              \
+  {                                                                                        \
+    constexpr int q_ = (GI) / (DVB / 4), d0_ = ((GI) % (DVB / 4)) * 4;                     \
+    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 0) * 64>(trb);               \
+    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 0) * 64>(trb);      \
+    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 1) * 64>(trb);               \
+    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 1) * 64>(trb);      \
+    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 2) * 64>(trb);               \
+    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 2) * 64>(trb);      \
+    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 3) * 64>(trb);               \
+    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 3) * 64>(trb);      \
+  }
+#define SAS_TR_MMA(GI, SRC)                                                                \
+  {                                                                                        \
+    constexpr int q_ = (GI) / (DVB / 4), d0_ = ((GI) % (DVB / 4)) * 4;                     \
+    _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                        \
+      const i16x8 aop = {SRC[2 * e][0],     SRC[2 * e][1],     SRC[2 * e][2],              \
+                         SRC[2 * e][3],     SRC[2 * e + 1][0], SRC[2 * e + 1][1],          \
+                         SRC[2 * e + 1][2], SRC[2 * e + 1][3]};                            \
+      acc[d0_ + e] = Ops::mma(aop, pk[q_], acc[d0_ + e]);                                  \
+    }                                                                                      \
+  }
+          SAS_TR_GROUP(0, gbuf[0]);
+          if constexpr (NG > 1) SAS_TR_GROUP(1, gbuf[1]);
+          if constexpr (NG > 1) lds_wait_group<8>(gbuf[0]); else lds_wait_group<0>(gbuf[0]);
+          SAS_TR_MMA(0, gbuf[0]);
+          if constexpr (NG > 2) SAS_TR_GROUP(2, gbuf[0]);
+          if constexpr (NG > 1) {
+            if constexpr (NG > 2) lds_wait_group<8>(gbuf[1]); else lds_wait_group<0>(gbuf[1]);
+            SAS_TR_MMA(1, gbuf[1]);
           }
+          if constexpr (NG > 3) SAS_TR_GROUP(3, gbuf[1]);
+          if constexpr (NG > 2) {
+            if constexpr (NG > 3) lds_wait_group<8>(gbuf[0]); else lds_wait_group<0>(gbuf[0]);
+            SAS_TR_MMA(2, gbuf[0]);
+          }
+          if constexpr (NG > 3) {
+            lds_wait_group<0>(gbuf[1]);
+            SAS_TR_MMA(3, gbuf[1]);
+          }
+          static_assert(NG <= 4, "pipeline written for up to 4 groups");
+#undef SAS_TR_GROUP
+#undef SAS_TR_MMA
         }
       }
       __syncthreads();  // rowid / tmask / ring are rewritten by the next chunk or item
@@ -507,15 +602,22 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
 // ---------------------------------------------------------------------------
 // Split-KV merge: lse = log(e^sink + Σ e^lse_i), out = Σ e^(lse_i - lse) o_i
 // ---------------------------------------------------------------------------
+constexpr int MERGE_MAX_PIECES = 32;  // pieces whose weights are staged in LDS
+constexpr int MERGE_MAX_HEADS = 64;
+
 template <int DV, typename T>
 __global__ __launch_bounds__(256) void merge_kernel(const SasAttnArgs a) {
+  __shared__ float wgt[MERGE_MAX_PIECES][MERGE_MAX_HEADS];
+  __shared__ float lse_out[MERGE_MAX_HEADS];
+  if (blockIdx.x >= (unsigned)a.num_fd) return;
   const int32_t* fd = a.metadata + SAS_FD_OFFSET + blockIdx.x * SAS_FD_METADATA_SIZE;
-  if (blockIdx.x >= (unsigned)a.num_fd || fd[0] == 0) return;
+  if (fd[0] == 0) return;
   const int mb = a.m_base;
   const int hblocks = (a.num_heads + mb - 1) / mb;
   const int b = fd[1], m = fd[2], slot0 = fd[3], npc = fd[4], h0 = fd[5], hn = fd[6];
   if (b < 0 || b >= a.batch || m < 0 || slot0 < 0 || npc < 1 ||
-      slot0 + npc > a.num_partial_slots || h0 < 0 || hn < 1 || h0 + hn > mb)
+      slot0 + npc > a.num_partial_slots || h0 < 0 || hn < 1 || h0 + hn > mb ||
+      hn > MERGE_MAX_HEADS)
     return;
   const int s = m / hblocks;
   const int hbase = (m - s * hblocks) * mb;
@@ -523,34 +625,54 @@ __global__ __launch_bounds__(256) void merge_kernel(const SasAttnArgs a) {
   if (tok < 0 || tok >= a.total_tokens) return;
   const float* wo = a.workspace;
   const float* wl = a.workspace + (size_t)a.num_partial_slots * mb * DV;
+  const bool staged = npc <= MERGE_MAX_PIECES;
+
+  // per head: lse = log(e^sink + sum_i e^lse_i); weights e^(lse_i - lse)
+  auto head_lse = [&](int hh) {
+    const int h = hbase + h0 + hh;
+    const float sink = h < a.num_heads ? a.sinks[h] : -INFINITY;
+    float mx = sink;
+    for (int i = 0; i < npc; ++i) mx = fmaxf(mx, wl[(size_t)(slot0 + i) * mb + h0 + hh]);
+    if (mx == -INFINITY) return -INFINITY;
+    float tot = __expf(sink - mx);
+    for (int i = 0; i < npc; ++i) tot += __expf(wl[(size_t)(slot0 + i) * mb + h0 + hh] - mx);
+    return mx + __logf(tot);
+  };
+  for (int hh = threadIdx.x; hh < hn; hh += blockDim.x) {
+    const float l = head_lse(hh);
+    lse_out[hh] = l;
+    if (staged)
+      for (int i = 0; i < npc; ++i) {
+        const float li = wl[(size_t)(slot0 + i) * mb + h0 + hh];
+        wgt[i][hh] = (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
+      }
+  }
+  __syncthreads();
+
   constexpr int V4 = DV / 4;
   for (int e = threadIdx.x; e < hn * V4; e += blockDim.x) {
-    const int hl = h0 + e / V4;   // head within the m-block
-    const int h = hbase + hl;     // absolute head
+    const int hh = e / V4;
+    const int c4 = e - hh * V4;
+    const int h = hbase + h0 + hh;
     if (h >= a.num_heads) continue;
-    const int c4 = e % V4;
-    const float sink = a.sinks[h];
-    float mx = sink;
-    for (int i = 0; i < npc; ++i) mx = fmaxf(mx, wl[(size_t)(slot0 + i) * mb + hl]);
+    const float l = lse_out[hh];
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    float lse = -INFINITY;
-    if (mx != -INFINITY) {
-      float tot = expf(sink - mx);
-      for (int i = 0; i < npc; ++i) tot += expf(wl[(size_t)(slot0 + i) * mb + hl] - mx);
-      lse = mx + logf(tot);
-      for (int i = 0; i < npc; ++i) {
-        const float li = wl[(size_t)(slot0 + i) * mb + hl];
-        if (li == -INFINITY) continue;
-        const float wgt = expf(li - lse);
-        const f32x4 v = *(const f32x4*)(wo + ((size_t)(slot0 + i) * mb + hl) * DV + 4 * c4);
-        o[0] += wgt * v[0]; o[1] += wgt * v[1]; o[2] += wgt * v[2]; o[3] += wgt * v[3];
+    for (int i = 0; i < npc; ++i) {
+      float wi;
+      if (staged) {
+        wi = wgt[i][hh];
+      } else {
+        const float li = wl[(size_t)(slot0 + i) * mb + h0 + hh];
+        wi = (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
       }
+      const f32x4 v = *(const f32x4*)(wo + ((size_t)(slot0 + i) * mb + h0 + hh) * DV + 4 * c4);
+      o[0] += wi * v[0]; o[1] += wi * v[1]; o[2] += wi * v[2]; o[3] += wi * v[3];
     }
     T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 4 * c4;
     const i16x4 pk = {MfmaOps<T>::from_f32(o[0]), MfmaOps<T>::from_f32(o[1]),
                       MfmaOps<T>::from_f32(o[2]), MfmaOps<T>::from_f32(o[3])};
     *(i16x4*)orow = pk;
-    if (c4 == 0) a.lse[(size_t)tok * a.num_heads + h] = lse;
+    if (c4 == 0) a.lse[(size_t)tok * a.num_heads + h] = l;
   }
 }
 
