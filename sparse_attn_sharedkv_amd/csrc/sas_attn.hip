@@ -116,9 +116,12 @@ __device__ inline float wave_max_pair(float v) {
 // Direct-to-LDS 16-byte loads: lane's data lands at M0 + lane * 16.
 // Issued through inline asm so the compiler does not serialise them against
 // unrelated LDS reads; completion is tracked by hand with s_waitcnt vmcnt.
+// An LDS DMA that reads M0 needs one wait state after the SALU write of M0
+// (the compiler's hazard pass cannot see inside the asm), hence the s_nop.
 __device__ inline void dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
   asm volatile(
       "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, %1\n\t" ::"v"(voff),
       "s"(sbase), "s"(lds_base)
       : "memory");
@@ -126,6 +129,7 @@ __device__ inline void dma16_sbase(const void* sbase, uint32_t voff, uint32_t ld
 __device__ inline void dma16_vaddr(const void* gptr, uint32_t lds_base) {
   asm volatile(
       "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, off\n\t" ::"v"(gptr),
       "s"(lds_base)
       : "memory");
@@ -160,29 +164,48 @@ __device__ inline void lds_wait_group(i16x4 (&r)[8]) {
 // ---------------------------------------------------------------------------
 // Attention kernel
 // ---------------------------------------------------------------------------
+// Waves: NHG head groups of 32 heads x 4 quarters = 4*NHG waves (two per SIMD
+// for NHG = 2). Wave w -> head group hg = w % NHG, quarter q = w / NHG.
+//   Q·Kᵀ: wave q computes a partial Sᵀ[32 rows x 32 heads] over dims quarter q
+//         (main dims 128q..128q+127 and, for d_qk 576, rope dims 512+16q..+15).
+//   reduce-scatter: the partials of a head group are summed through LDS; wave q
+//         owns the 8 rows {8q + 4*hl + 0..3} (hl = lane / 32) of the sum.
+//   softmax: on the 4 rows x 1 head a lane owns; P (rounded to the input type)
+//         is shared through LDS, so every wave of the head group sees all 32
+//         rows of P. Running max m is shared by the four waves; each keeps a
+//         partial row sum (fp32 P) that is combined once per item.
+//   P·V:  wave q accumulates Oᵀ[dv quarter q (128) x 32 heads] over all rows.
+// Per tile: barrier A (partials written; the oldest stage is free for the
+// next DMA) and barrier B (P written; this tile's successor has landed). A
+// rescale (some head's max grew by more than 2^8) is decided workgroup-wide
+// after B and costs one more barrier.
 template <int DQK, int DV, int NHG, typename T>
-__global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
-  constexpr int NSPLIT = 2;              // waves per head group (dims halves)
-  constexpr int NW = NSPLIT * NHG;       // waves per workgroup
+__global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
+  constexpr int NQ = 4;                  // dims / dv quarters per head group
+  constexpr int NW = NQ * NHG;           // waves per workgroup
   constexpr int MB = 32 * NHG;           // heads per item (m-block)
   constexpr int NT = 64 * NW;            // threads
   constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
   constexpr int ROWB = DQK * 2;          // bytes per cache row in HBM
-  constexpr int NKS_MAIN = 32 / NSPLIT;  // k-steps over this wave's 512/NSPLIT main dims
-  constexpr int NKS_ROPE = ROPE ? 4 / NSPLIT : 0;  // k-steps over its 64/NSPLIT rope dims
-  constexpr int NKS = NKS_MAIN + NKS_ROPE;
-  constexpr int DVB = DV / 32 / NSPLIT;  // 32-wide dv blocks per wave
+  constexpr int NKS_MAIN = 8;            // k-steps over 128 main dims
+  constexpr int NKS = NKS_MAIN + (ROPE ? 1 : 0);
+  constexpr int DVB = DV / 32 / NQ;      // 32-wide dv blocks per wave (4)
   constexpr int STAGE_BYTES = MAIN_BYTES + (ROPE ? ROPE_BYTES : 0);
   constexpr int ROWS_PER_WAVE = TILE / NW;            // main-part DMA instructions per wave
   constexpr int NROPE = ROPE ? TILE / 8 : 0;          // rope DMA instructions per tile
+  constexpr int PSTRIDE = 80;            // bytes per head in the P buffer (64 + pad)
   static_assert(DQK == 512 || DQK == 576, "head_dim");
   static_assert(DV == 512, "head_dim_v");
   static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
   static_assert(TILE % NW == 0, "rows per wave");
+  static_assert(DVB == 4, "two groups of four dv blocks per wave");
   typedef MfmaOps<T> Ops;
 
   __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTAGE * STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) f32x4 xchg[NW][4][64];
+  __shared__ __attribute__((aligned(16))) f32x4 xpart[NHG][NQ][NQ - 1][64];  // partial Sᵀ
+  __shared__ __attribute__((aligned(16))) unsigned char pbuf[NHG][32 * PSTRIDE];
+  __shared__ float mbuf[NHG][NQ][32];   // per-quarter row max (also the l combine)
+  __shared__ int flags[NW];
   __shared__ uint32_t rowid[RCHUNK];
   __shared__ uint32_t tmask[RCHUNK / TILE];
   __shared__ int first_neg;
@@ -191,25 +214,25 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hg = w % NHG;
-  const int p = w / NHG;
-  const int pw = (NSPLIT - 1 - p) * NHG + hg;  // partner wave (other dims half)
+  const int q = w / NHG;
   const int hlocal = hg * 32 + (lane & 31);  // head within the item's m-block
   const int hblocks = (a.num_heads + MB - 1) / MB;
-  const int hl = lane >> 5;                // 0: rows {0-3,8-11,..}, 1: rows {4-7,12-15,..}
+  const int hl = lane >> 5;
   const int my_rope_dma = (w < NROPE) ? ((NROPE - 1 - w) / NW + 1) : 0;
-  // this wave's dims: main chunks [MC p, MC p + MC), rope chunks 64 + [RC p, RC p + RC)
-  // Kᵀ operand: row lane%32, chunk MC p + 2 ks + hl (main) / 64 + RC p + 2 j + hl (rope)
-  constexpr int MC = 64 / NSPLIT, RC = 8 / NSPLIT;
+  // Kᵀ operand: row lane%32, main chunk 16q + 2ks + hl, rope chunk 64 + 2q + hl
   const int r_qk = lane & 31;
-  const int qk_base = main_row_base(r_qk) + (MC * p + hl) * 16;
-  int rope_off[NKS_ROPE > 0 ? NKS_ROPE : 1];
-#pragma unroll
-  for (int j = 0; j < NKS_ROPE; ++j) rope_off[j] = MAIN_BYTES + rope_slot(r_qk, RC * p + 2 * j + hl) * 16;
+  const int qk_base = main_row_base(r_qk) + (16 * q + hl) * 16;
+  const int rope_off = MAIN_BYTES + rope_slot(r_qk, 2 * q + hl) * 16;
   // Vᵀ operand (ds_read_b64_tr_b16): 16-lane group (lane>>4) reads rows
-  // 4*hl + (lane&15)/4 (+16q, +8) at dv p*DV/2 + 16*((lane>>4)&1) + 4*(lane&3) (+32d).
+  // 4*hl + (lane&15)/4 (+16k, +8) at dv 128q + 16*((lane>>4)&1) + 4*(lane&3) (+32d).
   // Row r+16 has the same rotation as r; row r+8 (r%8 < 4) has rotation +2.
-  const int tr_base = main_row_base(4 * hl + ((lane & 15) >> 2)) + p * (DV / NSPLIT) * 2 +
+  const int tr_base = main_row_base(4 * hl + ((lane & 15) >> 2)) + q * (DV / NQ) * 2 +
                       ((lane >> 4) & 1) * 32 + (lane & 3) * 8;
+  // P buffer: per head 32 bf16 in k-operand order. Position 16k + 8h + i holds
+  // row 16k + 4h + i (i < 4) or 16k + 8 + 4h + (i - 4), matching the Vᵀ reads.
+  // Wave q's rows 8q + 4hl + jj sit at 16(q/2) + 8hl + 4(q%2) + jj.
+  unsigned char* prow = &pbuf[hg][(lane & 31) * PSTRIDE];
+  const int pwr_off = (16 * (q >> 1) + 8 * hl + 4 * (q & 1)) * 2;
 
   // XCD-aware row mapping: consecutive FA rows (pieces of one item) share an XCD.
   const int nfa = a.num_fa;
@@ -258,12 +281,13 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
     const int p_hi = bhi * s2b < L ? bhi * s2b : L;
     const bool tok_ok = tok >= 0 && tok < a.total_tokens;
 
-    // query fragment for this wave's dims (B operand of Sᵀ = K·Qᵀ); loaded once
-    // per item, after the first gathers are in flight
+    // query fragment for this wave's dims (B operand of Sᵀ = K·Qᵀ)
     i16x8 qf[NKS];
-    // ---- online-softmax state (per lane: one head) ----
+    // ---- online-softmax state: m shared by the head group, l partial per wave ----
+    // (golden.py:156-160 seeds m = sink, l = 1: the 1 goes to one lane of quarter 0;
+    // the row sums of lanes l and l ^ 32 (same head) are added at the end)
     float m_run = partial ? -INFINITY : (head_ok ? a.sinks[head] * LOG2E : -INFINITY);
-    float l_run = partial ? 0.0f : 1.0f;
+    float l_part = (partial || q != 0 || hl != 0) ? 0.0f : 1.0f;
     f32x16 acc[DVB];
 #pragma unroll
     for (int d = 0; d < DVB; ++d)
@@ -369,12 +393,12 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
       };
       auto issue = [&](int tile, int stage) {
         const uint32_t sbase = kv_base + stage * STAGE_BYTES;
-        // lane m holds the row id of this wave's m-th row of the tile
+        // lane j holds the row id of this wave's j-th row of the tile
         const uint32_t my_ids = rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)];
 #pragma unroll
-        for (int m = 0; m < ROWS_PER_WAVE; ++m) {
-          const int r = w + NW * m;
-          const uint32_t id = __builtin_amdgcn_readlane(my_ids, m);
+        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
+          const int r = w + NW * j;
+          const uint32_t id = __builtin_amdgcn_readlane(my_ids, j);
           dma16_sbase(row_ptr(id), (uint32_t)lane * 16u, sbase + main_row_base(r));
         }
         if (ROPE) {
@@ -410,32 +434,27 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
                                                  (head_ok ? head : 0)) * DQK;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-          const int dim = ks < NKS_MAIN ? ((512 / NSPLIT) * p + 16 * ks + 8 * hl)
-                                        : (512 + (64 / NSPLIT) * p + 16 * (ks - NKS_MAIN) + 8 * hl);
+          const int dim = ks < NKS_MAIN ? (128 * q + 16 * ks + 8 * hl) : (512 + 16 * q + 8 * hl);
           i16x8 v = *(const i16x8*)(qrow + dim);
           qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
         }
-        // A wait the compiler can see: it clears its pending-load state here, so it
-        // puts no vmcnt wait for qf inside the tile loop (that wait would also drain
-        // the row DMAs in flight on every tile). Also lands tiles 0 and 1.
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
       }
+      // A wait the compiler can see: it clears its pending-load state here, so it
+      // puts no vmcnt wait for qf inside the tile loop (that wait would also drain
+      // the row DMAs in flight on every tile). Also lands tiles 0 and 1.
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+      __syncthreads();
 
       for (int it = 0; it < ntile; ++it) {
         const int stage = it % NSTAGE;
-        wait_tile(it + 1 < ntile);
-        __syncthreads();
-        if (it + 2 < ntile) issue(it + 2, (it + 2) % NSTAGE);
-
         const unsigned char* sb = kv_lds + stage * STAGE_BYTES;
-        // ---- Sᵀ partial over this wave's dims (K operands prefetched 3 deep) ----
+        // ---- Sᵀ partial over this wave's dims quarter (K operands 3 deep) ----
         f32x16 st;
 #pragma unroll
         for (int j = 0; j < 16; ++j) st[j] = 0.0f;
         {
           auto kaddr = [&](int ks) -> const i16x8* {
-            return (const i16x8*)(ks < NKS_MAIN ? sb + qk_base + ks * 32
-                                                : sb + rope_off[ks - NKS_MAIN]);
+            return (const i16x8*)(ks < NKS_MAIN ? sb + qk_base + ks * 32 : sb + rope_off);
           };
           constexpr int PF = 3;
           i16x8 kbuf[PF];
@@ -448,111 +467,129 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
             st = Ops::mma(kop, qf[ks], st);
           }
         }
-        {
-          // ---- sum the two dims halves through LDS ----
-  #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            xchg[w][q4][lane] = (f32x4){st[4 * q4], st[4 * q4 + 1], st[4 * q4 + 2], st[4 * q4 + 3]};
-          __syncthreads();
-  #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const f32x4 o = xchg[pw][q4][lane];
-            // identical operand order in both waves -> bitwise identical sums
-            if (p == 0) {
-              st[4 * q4] += o[0]; st[4 * q4 + 1] += o[1]; st[4 * q4 + 2] += o[2]; st[4 * q4 + 3] += o[3];
-            } else {
-              st[4 * q4] = o[0] + st[4 * q4]; st[4 * q4 + 1] = o[1] + st[4 * q4 + 1];
-              st[4 * q4 + 2] = o[2] + st[4 * q4 + 2]; st[4 * q4 + 3] = o[3] + st[4 * q4 + 3];
-            }
+        // ---- reduce-scatter of the partials: quarter G's rows go to wave G ----
+#pragma unroll
+        for (int G = 0; G < NQ; ++G)
+          if (G != q)
+            xpart[hg][G][q < G ? q : q - 1][lane] =
+                (f32x4){st[4 * G], st[4 * G + 1], st[4 * G + 2], st[4 * G + 3]};
+        __syncthreads();  // barrier A
+        if (it + 2 < ntile) issue(it + 2, (it + 2) % NSTAGE);
+
+        f32x4 own;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          own[e] = q == 0 ? st[e] : q == 1 ? st[4 + e] : q == 2 ? st[8 + e] : st[12 + e];
+        const f32x4 x0 = xpart[hg][q][0][lane];
+        const f32x4 x1 = xpart[hg][q][1][lane];
+        const f32x4 x2 = xpart[hg][q][2][lane];
+        // fixed summation order over source quarters 0, 1, 2, 3
+        const f32x4 t0 = q == 0 ? own : x0;
+        const f32x4 t1 = q == 1 ? own : (q == 0 ? x0 : x1);
+        const f32x4 t2 = q == 2 ? own : (q < 2 ? x1 : x2);
+        const f32x4 t3 = q == 3 ? own : x2;
+        const f32x4 sred = ((t0 + t1) + t2) + t3;
+
+        // ---- online softmax (exp2 domain) on rows 8q + 4hl + jj ----
+        const uint32_t vm = tmask[it] >> (8 * q + 4 * hl);
+        float sv[4];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sv[e] = ((vm >> e) & 1u) ? sred[e] * sc : -INFINITY;
+          mloc = fmaxf(mloc, sv[e]);
+        }
+        mloc = wave_max_pair(mloc);
+        if (hl == 0) mbuf[hg][q][lane & 31] = mloc;
+        const bool need_any = __any(mloc > m_run + RESCALE_TAU);
+        if (lane == 0) flags[w] = need_any ? 1 : 0;
+        float pv[4];
+        auto make_p = [&]() {
+          i16x4 pk4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pv[e] = (sv[e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sv[e] - m_run);
+            pk4[e] = Ops::from_f32(pv[e]);
           }
-        }
+          *(i16x4*)(prow + pwr_off) = pk4;
+        };
+        make_p();
+        wait_tile(it + 2 < ntile);  // this wave's share of tile it + 1 has landed
+        __syncthreads();            // barrier B
 
-        // ---- online softmax (exp2 domain), in place on the Sᵀ accumulator ----
-        const uint32_t vm = tmask[it];
-        float mx = -INFINITY;
+        int anyf = 0;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int row = 8 * (j >> 2) + 4 * hl + (j & 3);
-          st[j] = ((vm >> row) & 1u) ? st[j] * sc : -INFINITY;
-          mx = fmaxf(mx, st[j]);
+        for (int i = 0; i < NW; ++i) anyf |= flags[i];
+        if (__builtin_amdgcn_readfirstlane(anyf)) {
+          // rescale: every wave of the head group derives the same new max
+          float mt = mbuf[hg][0][lane & 31];
+#pragma unroll
+          for (int i = 1; i < NQ; ++i) mt = fmaxf(mt, mbuf[hg][i][lane & 31]);
+          if (mt > m_run + RESCALE_TAU) {
+            const float m2 = fmaxf(m_run, mt);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m2);  // m_run = -inf -> 0
+            l_part *= alpha;
+#pragma unroll
+            for (int d = 0; d < DVB; ++d)
+#pragma unroll
+              for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
+            m_run = m2;
+          }
+          make_p();         // nobody has read P yet: rewrite this wave's rows
+          __syncthreads();  // barrier C
         }
-        mx = wave_max_pair(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const bool need = m_new > m_run + RESCALE_TAU;
-        if (__any(need)) {
-          const float m2 = need ? m_new : m_run;
-          const float alpha = (m2 == m_run) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m2);
-          l_run *= alpha;
-#pragma unroll
-          for (int d = 0; d < DVB; ++d)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
-          m_run = m2;
-        }
-        float psum = 0.0f;
+        l_part += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+
+        // ---- Oᵀ += Vᵀ · Pᵀ over both 16-row k-steps ----
         i16x8 pk[2];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float pv = (st[j] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(st[j] - m_run);
-          psum += pv;
-          pk[j >> 3][j & 7] = Ops::from_f32(pv);
-        }
-        psum += __shfl_xor(psum, 32);
-        l_run += psum;
-
-        // ---- Oᵀ += Vᵀ · Pᵀ: groups of 4 dv blocks (8 transposed reads), double-buffered ----
+        pk[0] = *(const i16x8*)(prow + 16 * hl);
+        pk[1] = *(const i16x8*)(prow + 32 + 16 * hl);
         {
-          static_assert(DVB % 4 == 0, "dv blocks come in groups of 4");
-          constexpr int NG = 2 * DVB / 4;  // groups: (q, d0..d0+3)
+          constexpr int NG = 2;  // groups: (k-step kq, dv blocks 0..3)
           const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
           i16x4 gbuf[2][8];
 #define SAS_TR_GROUP(GI, DST)                                                              \
   {                                                                                        \
-    constexpr int q_ = (GI) / (DVB / 4), d0_ = ((GI) % (DVB / 4)) * 4;                     \
-    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 0) * 64>(trb);               \
-    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 0) * 64>(trb);      \
-    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 1) * 64>(trb);               \
-    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 1) * 64>(trb);      \
-    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 2) * 64>(trb);               \
-    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 2) * 64>(trb);      \
-    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + (d0_ + 3) * 64>(trb);               \
-    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + (d0_ + 3) * 64>(trb);      \
+    constexpr int q_ = (GI);                                                               \
+    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 0 * 64>(trb);                       \
+    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 0 * 64>(trb);              \
+    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 1 * 64>(trb);                       \
+    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 1 * 64>(trb);              \
+    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 2 * 64>(trb);                       \
+    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 2 * 64>(trb);              \
+    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 3 * 64>(trb);                       \
+    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 3 * 64>(trb);              \
   }
 #define SAS_TR_MMA(GI, SRC)                                                                \
   {                                                                                        \
-    constexpr int q_ = (GI) / (DVB / 4), d0_ = ((GI) % (DVB / 4)) * 4;                     \
     _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                        \
       const i16x8 aop = {SRC[2 * e][0],     SRC[2 * e][1],     SRC[2 * e][2],              \
                          SRC[2 * e][3],     SRC[2 * e + 1][0], SRC[2 * e + 1][1],          \
                          SRC[2 * e + 1][2], SRC[2 * e + 1][3]};                            \
-      acc[d0_ + e] = Ops::mma(aop, pk[q_], acc[d0_ + e]);                                  \
+      acc[e] = Ops::mma(aop, pk[(GI)], acc[e]);                                            \
     }                                                                                      \
   }
           SAS_TR_GROUP(0, gbuf[0]);
-          if constexpr (NG > 1) SAS_TR_GROUP(1, gbuf[1]);
-          if constexpr (NG > 1) lds_wait_group<8>(gbuf[0]); else lds_wait_group<0>(gbuf[0]);
+          SAS_TR_GROUP(1, gbuf[1]);
+          lds_wait_group<8>(gbuf[0]);
           SAS_TR_MMA(0, gbuf[0]);
-          if constexpr (NG > 2) SAS_TR_GROUP(2, gbuf[0]);
-          if constexpr (NG > 1) {
-            if constexpr (NG > 2) lds_wait_group<8>(gbuf[1]); else lds_wait_group<0>(gbuf[1]);
-            SAS_TR_MMA(1, gbuf[1]);
-          }
-          if constexpr (NG > 3) SAS_TR_GROUP(3, gbuf[1]);
-          if constexpr (NG > 2) {
-            if constexpr (NG > 3) lds_wait_group<8>(gbuf[0]); else lds_wait_group<0>(gbuf[0]);
-            SAS_TR_MMA(2, gbuf[0]);
-          }
-          if constexpr (NG > 3) {
-            lds_wait_group<0>(gbuf[1]);
-            SAS_TR_MMA(3, gbuf[1]);
-          }
-          static_assert(NG <= 4, "pipeline written for up to 4 groups");
+          lds_wait_group<0>(gbuf[1]);
+          SAS_TR_MMA(1, gbuf[1]);
+          static_assert(NG == 2, "two k-steps per 32-row tile");
 #undef SAS_TR_GROUP
 #undef SAS_TR_MMA
         }
       }
       __syncthreads();  // rowid / tmask / ring are rewritten by the next chunk or item
     }
+
+    // ---- combine the row sums of the four quarters (fixed order) ----
+    l_part += __shfl_xor(l_part, 32);
+    if (hl == 0) mbuf[hg][q][lane & 31] = l_part;
+    __syncthreads();
+    const float l_run = ((mbuf[hg][0][lane & 31] + mbuf[hg][1][lane & 31]) +
+                         mbuf[hg][2][lane & 31]) + mbuf[hg][3][lane & 31];
+    __syncthreads();  // mbuf is reused by the next item
 
     // ---- epilogue ----
     if (tok_ok && head_ok) {
@@ -563,14 +600,14 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
         for (int d = 0; d < DVB; ++d)
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
-            const int dv = p * (DV / NSPLIT) + 32 * d + 8 * g4 + 4 * hl;
+            const int dv = q * (DV / NQ) + 32 * d + 8 * g4 + 4 * hl;
             const i16x4 v = {Ops::from_f32(acc[d][4 * g4] * inv),
                              Ops::from_f32(acc[d][4 * g4 + 1] * inv),
                              Ops::from_f32(acc[d][4 * g4 + 2] * inv),
                              Ops::from_f32(acc[d][4 * g4 + 3] * inv)};
             *(i16x4*)(orow + dv) = v;
           }
-        if (p == 0 && hl == 0) a.lse[(size_t)tok * a.num_heads + head] = (m_run + __log2f(l_run)) * LN2;
+        if (q == 0 && hl == 0) a.lse[(size_t)tok * a.num_heads + head] = (m_run + __log2f(l_run)) * LN2;
       } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
         float* wo = a.workspace + ((size_t)slot * MB + hlocal) * DV;
         const bool empty = !(l_run > 0.0f);
@@ -579,13 +616,13 @@ __global__ __launch_bounds__(128 * NHG) void attn_kernel(const SasAttnArgs a) {
         for (int d = 0; d < DVB; ++d)
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
-            const int dv = p * (DV / NSPLIT) + 32 * d + 8 * g4 + 4 * hl;
+            const int dv = q * (DV / NQ) + 32 * d + 8 * g4 + 4 * hl;
             f32x4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = acc[d][4 * g4 + e] * inv;
             *(f32x4*)(wo + dv) = v;
           }
-        if (p == 0 && hl == 0) {
+        if (q == 0 && hl == 0) {
           float* wl = a.workspace + (size_t)a.num_partial_slots * MB * DV;
           wl[(size_t)slot * MB + hlocal] =
               empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
@@ -681,7 +718,7 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   const int phases = a.phases == 0 ? 3 : a.phases;
   if (phases & 1) {
     const int per_xcd = (a.num_fa + 7) / 8;
-    hipLaunchKernelGGL((attn_kernel<DQK, 512, NHG, T>), dim3(8 * per_xcd), dim3(128 * NHG), 0,
+    hipLaunchKernelGGL((attn_kernel<DQK, 512, NHG, T>), dim3(8 * per_xcd), dim3(256 * NHG), 0,
                        st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -693,8 +730,8 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
-// Items carry m_base = 32 or 64 heads (one or two 32-head groups, each a
-// dims-split wave pair): 2 or 4 waves, one wave per SIMD.
+// Items carry m_base = 32 or 64 heads (one or two 32-head groups of four
+// dims-quarter waves): 4 or 8 waves, one or two per SIMD.
 template <typename T>
 static hipError_t dispatch_heads(const SasAttnArgs& a, hipStream_t st) {
   if (a.head_dim == 576)
