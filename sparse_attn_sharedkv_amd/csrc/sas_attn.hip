@@ -108,9 +108,15 @@ __device__ __host__ inline int row_rot(int r) { return (r >> 2) & 3; }
 __device__ __host__ inline int main_row_base(int r) { return r * MAIN_ROW_BYTES + row_rot(r) * 16; }
 __device__ __host__ inline int rope_slot(int r, int cr) { return 8 * r + ((cr + (r >> 1)) & 7); }
 
+// Combine lane l with lane l ^ 32 in registers (v_permlane32_swap): both
+// halves end up with the identical result.
 __device__ inline float wave_max_pair(float v) {
-  // combine lane l with lane l ^ 32
-  return fmaxf(v, __shfl_xor(v, 32));
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float wave_sum_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);  // lower half + upper half
 }
 
 // Direct-to-LDS 16-byte loads: lane's data lands at M0 + lane * 16.
@@ -199,13 +205,14 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
   static_assert(TILE % NW == 0, "rows per wave");
   static_assert(DVB == 4, "two groups of four dv blocks per wave");
+  static_assert(NROPE <= NW, "at most one rope DMA instruction per wave");
   typedef MfmaOps<T> Ops;
 
   __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTAGE * STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) f32x4 xpart[NHG][NQ][NQ - 1][64];  // partial Sᵀ
+  __shared__ __attribute__((aligned(16))) f32x4 xpart[NHG][NQ][NQ][64];  // partial Sᵀ [dest][src]
   __shared__ __attribute__((aligned(16))) unsigned char pbuf[NHG][32 * PSTRIDE];
   __shared__ float mbuf[NHG][NQ][32];   // per-quarter row max (also the l combine)
-  __shared__ int flags[NW];
+  __shared__ __attribute__((aligned(8))) unsigned char flags[8];  // per-wave rescale votes
   __shared__ uint32_t rowid[RCHUNK];
   __shared__ uint32_t tmask[RCHUNK / TILE];
   __shared__ int first_neg;
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   const int hlocal = hg * 32 + (lane & 31);  // head within the item's m-block
   const int hblocks = (a.num_heads + MB - 1) / MB;
   const int hl = lane >> 5;
-  const int my_rope_dma = (w < NROPE) ? ((NROPE - 1 - w) / NW + 1) : 0;
+  const int my_rope_dma = (w < NROPE) ? 1 : 0;
   // Kᵀ operand: row lane%32, main chunk 16q + 2ks + hl, rope chunk 64 + 2q + hl
   const int r_qk = lane & 31;
   const int qk_base = main_row_base(r_qk) + (16 * q + hl) * 16;
@@ -251,6 +258,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   const char* ori_kv = (const char*)a.ori_kv;
   const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
   const float sc = a.softmax_scale * LOG2E;
+  if (tid < 8) flags[tid] = 0;  // bytes of absent waves stay 0
 
   bool first_item = true;
   for (;;) {
@@ -374,7 +382,8 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
             id = (uint32_t)(phys * a.cmp_block_size + cid[e] % a.cmp_block_size) | 0x80000000u;
           }
         }
-        rowid[r] = id;
+        // masked rows still get a DMA: point them at row 0 of the original cache
+        rowid[r] = id == ROW_INVALID ? 0u : id;
         const unsigned long long bal = __ballot(id != ROW_INVALID);
         if (lane == 0) {
           tmask[(r - lane) / TILE] = (uint32_t)bal;
@@ -386,32 +395,33 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       // ---- DMA issue for one tile into one ring stage ----
       // main part: wave w fills rows w, w + NW, ...; one 1 KB row per instruction
       // rope part: instruction i fills rows 8i..8i+7 (8 lanes per row)
+      // branch-free row address (bit 31 of the id selects the compressed cache)
       auto row_ptr = [&](uint32_t id) -> const char* {
-        if (id == ROW_INVALID) return ori_kv;  // masked row: any in-bounds address
-        return (id & 0x80000000u) ? cmp_kv + (size_t)(id & 0x7FFFFFFFu) * ROWB
-                                  : ori_kv + (size_t)id * ROWB;
+        const char* base = (id & 0x80000000u) ? cmp_kv : ori_kv;
+        return base + (size_t)(id & 0x7FFFFFFFu) * ROWB;
       };
-      auto issue = [&](int tile, int stage) {
+      // row ids a wave needs to issue one tile: lane j < ROWS_PER_WAVE holds the
+      // id of its j-th main row; for the rope instruction (waves w < NROPE) lane
+      // l holds the id of row 8w + l/8. Read ahead of use to hide LDS latency.
+      auto main_ids = [&](int tile) -> uint32_t {
+        return rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)];
+      };
+      auto rope_ids = [&](int tile) -> uint32_t {
+        return ROPE && w < NROPE ? rowid[tile * TILE + 8 * w + (lane >> 3)] : 0u;
+      };
+      auto issue = [&](int stage, uint32_t my_ids, uint32_t rope_id) {
         const uint32_t sbase = kv_base + stage * STAGE_BYTES;
-        // lane j holds the row id of this wave's j-th row of the tile
-        const uint32_t my_ids = rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)];
 #pragma unroll
         for (int j = 0; j < ROWS_PER_WAVE; ++j) {
           const int r = w + NW * j;
           const uint32_t id = __builtin_amdgcn_readlane(my_ids, j);
           dma16_sbase(row_ptr(id), (uint32_t)lane * 16u, sbase + main_row_base(r));
         }
-        if (ROPE) {
-#pragma unroll
-          for (int i0 = 0; i0 < NROPE; i0 += NW) {
-            const int i = i0 + w;
-            if (i < NROPE) {
-              const int r = 8 * i + (lane >> 3);
-              const int cr = ((lane & 7) - (r >> 1)) & 7;
-              const char* src = row_ptr(rowid[tile * TILE + r]) + 1024 + cr * 16;
-              dma16_vaddr(src, sbase + MAIN_BYTES + i * 1024);
-            }
-          }
+        if (ROPE && w < NROPE) {
+          const int r = 8 * w + (lane >> 3);
+          const int cr = ((lane & 7) - (r >> 1)) & 7;
+          const char* src = row_ptr(rope_id) + 1024 + cr * 16;
+          dma16_vaddr(src, sbase + MAIN_BYTES + w * 1024);
         }
       };
       // waits until at most the next tile's DMA instructions of this wave are in flight
@@ -427,8 +437,8 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         }
       };
 
-      issue(0, 0);
-      if (ntile > 1) issue(1, 1);
+      issue(0, main_ids(0), rope_ids(0));
+      if (ntile > 1) issue(1, main_ids(1), rope_ids(1));
       if (c0 == p_lo) {
         const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
                                                  (head_ok ? head : 0)) * DQK;
@@ -448,6 +458,11 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       for (int it = 0; it < ntile; ++it) {
         const int stage = it % NSTAGE;
         const unsigned char* sb = kv_lds + stage * STAGE_BYTES;
+        // LDS words needed later in this tile, read now (latency hidden by Q·Kᵀ)
+        const bool more = it + 2 < ntile;
+        const uint32_t vm_tile = tmask[it];
+        const uint32_t nx_main = main_ids(more ? it + 2 : it);
+        const uint32_t nx_rope = rope_ids(more ? it + 2 : it);
         // ---- Sᵀ partial over this wave's dims quarter (K operands 3 deep) ----
         f32x16 st;
 #pragma unroll
@@ -470,28 +485,16 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         // ---- reduce-scatter of the partials: quarter G's rows go to wave G ----
 #pragma unroll
         for (int G = 0; G < NQ; ++G)
-          if (G != q)
-            xpart[hg][G][q < G ? q : q - 1][lane] =
-                (f32x4){st[4 * G], st[4 * G + 1], st[4 * G + 2], st[4 * G + 3]};
+          xpart[hg][G][q][lane] = (f32x4){st[4 * G], st[4 * G + 1], st[4 * G + 2], st[4 * G + 3]};
         __syncthreads();  // barrier A
-        if (it + 2 < ntile) issue(it + 2, (it + 2) % NSTAGE);
+        if (more) issue((it + 2) % NSTAGE, nx_main, nx_rope);
 
-        f32x4 own;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          own[e] = q == 0 ? st[e] : q == 1 ? st[4 + e] : q == 2 ? st[8 + e] : st[12 + e];
-        const f32x4 x0 = xpart[hg][q][0][lane];
-        const f32x4 x1 = xpart[hg][q][1][lane];
-        const f32x4 x2 = xpart[hg][q][2][lane];
         // fixed summation order over source quarters 0, 1, 2, 3
-        const f32x4 t0 = q == 0 ? own : x0;
-        const f32x4 t1 = q == 1 ? own : (q == 0 ? x0 : x1);
-        const f32x4 t2 = q == 2 ? own : (q < 2 ? x1 : x2);
-        const f32x4 t3 = q == 3 ? own : x2;
-        const f32x4 sred = ((t0 + t1) + t2) + t3;
+        const f32x4 sred = ((xpart[hg][q][0][lane] + xpart[hg][q][1][lane]) +
+                            xpart[hg][q][2][lane]) + xpart[hg][q][3][lane];
 
         // ---- online softmax (exp2 domain) on rows 8q + 4hl + jj ----
-        const uint32_t vm = tmask[it] >> (8 * q + 4 * hl);
+        const uint32_t vm = vm_tile >> (8 * q + 4 * hl);
         float sv[4];
         float mloc = -INFINITY;
 #pragma unroll
@@ -514,13 +517,15 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           *(i16x4*)(prow + pwr_off) = pk4;
         };
         make_p();
-        wait_tile(it + 2 < ntile);  // this wave's share of tile it + 1 has landed
-        __syncthreads();            // barrier B
+        wait_tile(more);  // this wave's share of tile it + 1 has landed
+        __syncthreads();  // barrier B
 
-        int anyf = 0;
-#pragma unroll
-        for (int i = 0; i < NW; ++i) anyf |= flags[i];
-        if (__builtin_amdgcn_readfirstlane(anyf)) {
+        // P operand of both k-steps and the rescale votes, in one round trip
+        i16x8 pk[2];
+        pk[0] = *(const i16x8*)(prow + 16 * hl);
+        pk[1] = *(const i16x8*)(prow + 32 + 16 * hl);
+        const uint64_t votes = *(const uint64_t*)flags;
+        if (__builtin_amdgcn_readfirstlane((uint32_t)(votes | (votes >> 32)))) {
           // rescale: every wave of the head group derives the same new max
           float mt = mbuf[hg][0][lane & 31];
 #pragma unroll
@@ -535,15 +540,14 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
               for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
             m_run = m2;
           }
-          make_p();         // nobody has read P yet: rewrite this wave's rows
-          __syncthreads();  // barrier C
+          make_p();         // rewrite this wave's rows with the new max (the P
+          __syncthreads();  // read above is void and is repeated after barrier C)
+          pk[0] = *(const i16x8*)(prow + 16 * hl);
+          pk[1] = *(const i16x8*)(prow + 32 + 16 * hl);
         }
         l_part += (pv[0] + pv[1]) + (pv[2] + pv[3]);
 
         // ---- Oᵀ += Vᵀ · Pᵀ over both 16-row k-steps ----
-        i16x8 pk[2];
-        pk[0] = *(const i16x8*)(prow + 16 * hl);
-        pk[1] = *(const i16x8*)(prow + 32 + 16 * hl);
         {
           constexpr int NG = 2;  // groups: (k-step kq, dv blocks 0..3)
           const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
@@ -584,7 +588,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
     }
 
     // ---- combine the row sums of the four quarters (fixed order) ----
-    l_part += __shfl_xor(l_part, 32);
+    l_part = wave_sum_pair(l_part);
     if (hl == 0) mbuf[hg][q][lane & 31] = l_part;
     __syncthreads();
     const float l_run = ((mbuf[hg][0][lane & 31] + mbuf[hg][1][lane & 31]) +
