@@ -643,13 +643,21 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
 // ---------------------------------------------------------------------------
 // Split-KV merge: lse = log(e^sink + Σ e^lse_i), out = Σ e^(lse_i - lse) o_i
 // ---------------------------------------------------------------------------
+// Grid: (merge task, group of MERGE_HPB heads). Each thread owns MERGE_PER
+// float4 of the group's rows and issues all of one piece's loads before using
+// them, so the pass is bandwidth- rather than latency-bound.
 constexpr int MERGE_MAX_PIECES = 32;  // pieces whose weights are staged in LDS
-constexpr int MERGE_MAX_HEADS = 64;
+constexpr int MERGE_HPB = 8;          // heads per workgroup
+constexpr int MERGE_THREADS = 256;
 
 template <int DV, typename T>
-__global__ __launch_bounds__(256) void merge_kernel(const SasAttnArgs a) {
-  __shared__ float wgt[MERGE_MAX_PIECES][MERGE_MAX_HEADS];
-  __shared__ float lse_out[MERGE_MAX_HEADS];
+__global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs a) {
+  constexpr int V4 = DV / 4;                              // float4 per head row
+  constexpr int PER = MERGE_HPB * V4 / MERGE_THREADS;     // float4 per thread
+  static_assert(MERGE_HPB * V4 % MERGE_THREADS == 0, "merge tiling");
+  static_assert(MERGE_MAX_PIECES * MERGE_HPB <= MERGE_THREADS, "one piece lse per thread");
+  __shared__ float lse_p[MERGE_MAX_PIECES][MERGE_HPB];  // piece lse, then piece weight
+  __shared__ float lse_s[MERGE_HPB];
   if (blockIdx.x >= (unsigned)a.num_fd) return;
   const int32_t* fd = a.metadata + SAS_FD_OFFSET + blockIdx.x * SAS_FD_METADATA_SIZE;
   if (fd[0] == 0) return;
@@ -657,63 +665,110 @@ __global__ __launch_bounds__(256) void merge_kernel(const SasAttnArgs a) {
   const int hblocks = (a.num_heads + mb - 1) / mb;
   const int b = fd[1], m = fd[2], slot0 = fd[3], npc = fd[4], h0 = fd[5], hn = fd[6];
   if (b < 0 || b >= a.batch || m < 0 || slot0 < 0 || npc < 1 ||
-      slot0 + npc > a.num_partial_slots || h0 < 0 || hn < 1 || h0 + hn > mb ||
-      hn > MERGE_MAX_HEADS)
+      slot0 + npc > a.num_partial_slots || h0 < 0 || hn < 1 || h0 + hn > mb)
     return;
+  const int g0 = (int)blockIdx.y * MERGE_HPB;  // first head of this group within the task
+  if (g0 >= hn) return;
   const int s = m / hblocks;
-  const int hbase = (m - s * hblocks) * mb;
+  const int hbase = (m - s * hblocks) * mb + h0 + g0;  // query head of group row 0
+  const int hloc = h0 + g0;                            // m-block slot of group row 0
   const int tok = a.q_prefix[b] + s;
   if (tok < 0 || tok >= a.total_tokens) return;
   const float* wo = a.workspace;
   const float* wl = a.workspace + (size_t)a.num_partial_slots * mb * DV;
-  const bool staged = npc <= MERGE_MAX_PIECES;
+  const int tid = threadIdx.x;
+  const int nst = npc < MERGE_MAX_PIECES ? npc : MERGE_MAX_PIECES;  // pieces staged in LDS
 
-  // per head: lse = log(e^sink + sum_i e^lse_i); weights e^(lse_i - lse)
-  auto head_lse = [&](int hh) {
-    const int h = hbase + h0 + hh;
-    const float sink = h < a.num_heads ? a.sinks[h] : -INFINITY;
-    float mx = sink;
-    for (int i = 0; i < npc; ++i) mx = fmaxf(mx, wl[(size_t)(slot0 + i) * mb + h0 + hh]);
-    if (mx == -INFINITY) return -INFINITY;
-    float tot = __expf(sink - mx);
-    for (int i = 0; i < npc; ++i) tot += __expf(wl[(size_t)(slot0 + i) * mb + h0 + hh] - mx);
-    return mx + __logf(tot);
+  int hh_of[PER], c4_of[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int e = tid + MERGE_THREADS * k;
+    hh_of[k] = e / V4;
+    c4_of[k] = e - hh_of[k] * V4;
+  }
+  // rows past the task's last head (never stored) read that head's row instead
+  int hr_of[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) hr_of[k] = g0 + hh_of[k] < hn ? hh_of[k] : hn - 1 - g0;
+  auto piece = [&](int i, f32x4 (&v)[PER]) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k)  // all of one piece's loads in flight together
+      v[k] = *(const f32x4*)(wo + ((size_t)(slot0 + i) * mb + hloc + hr_of[k]) * DV + 4 * c4_of[k]);
   };
-  for (int hh = threadIdx.x; hh < hn; hh += blockDim.x) {
-    const float l = head_lse(hh);
-    lse_out[hh] = l;
-    if (staged)
-      for (int i = 0; i < npc; ++i) {
-        const float li = wl[(size_t)(slot0 + i) * mb + h0 + hh];
-        wgt[i][hh] = (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
-      }
+  // the first two pieces are fetched before the weights are known
+  f32x4 v0[PER], v1[PER];
+  piece(0, v0);
+  if (npc > 1) piece(1, v1);
+
+  // piece lse values: thread (i, hh) for i < nst, one load round
+  if (tid < nst * MERGE_HPB) {
+    const int i = tid / MERGE_HPB, hh = tid - i * MERGE_HPB;
+    lse_p[i][hh] = (g0 + hh < hn) ? wl[(size_t)(slot0 + i) * mb + hloc + hh] : -INFINITY;
+  }
+  __syncthreads();
+  // per head: lse = log(e^sink + Σ_i e^lse_i); weights e^(lse_i - lse)
+  if (tid < MERGE_HPB) {
+    const int hh = tid;
+    const int h = hbase + hh;
+    float l = -INFINITY;
+    if (g0 + hh < hn && h < a.num_heads) {
+      const float sink = a.sinks[h];
+      float mx = sink;
+      for (int i = 0; i < nst; ++i) mx = fmaxf(mx, lse_p[i][hh]);
+      for (int i = nst; i < npc; ++i) mx = fmaxf(mx, wl[(size_t)(slot0 + i) * mb + hloc + hh]);
+      float tot = __expf(sink - mx);
+      for (int i = 0; i < nst; ++i) tot += __expf(lse_p[i][hh] - mx);
+      for (int i = nst; i < npc; ++i) tot += __expf(wl[(size_t)(slot0 + i) * mb + hloc + hh] - mx);
+      l = mx + __logf(tot);
+    }
+    lse_s[hh] = l;
+    for (int i = 0; i < nst; ++i) {
+      const float li = lse_p[i][hh];
+      lse_p[i][hh] = (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
+    }
   }
   __syncthreads();
 
-  constexpr int V4 = DV / 4;
-  for (int e = threadIdx.x; e < hn * V4; e += blockDim.x) {
-    const int hh = e / V4;
-    const int c4 = e - hh * V4;
-    const int h = hbase + h0 + hh;
-    if (h >= a.num_heads) continue;
-    const float l = lse_out[hh];
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < npc; ++i) {
-      float wi;
-      if (staged) {
-        wi = wgt[i][hh];
-      } else {
-        const float li = wl[(size_t)(slot0 + i) * mb + h0 + hh];
-        wi = (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
-      }
-      const f32x4 v = *(const f32x4*)(wo + ((size_t)(slot0 + i) * mb + h0 + hh) * DV + 4 * c4);
-      o[0] += wi * v[0]; o[1] += wi * v[1]; o[2] += wi * v[2]; o[3] += wi * v[3];
+  auto weight = [&](int i, int hh) -> float {
+    if (i < MERGE_MAX_PIECES) return lse_p[i][hh];
+    const float l = lse_s[hh];
+    const float li = wl[(size_t)(slot0 + i) * mb + hloc + hh];
+    return (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
+  };
+  f32x4 o[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const float w0 = weight(0, hh_of[k]);
+    o[k] = (f32x4){w0 * v0[k][0], w0 * v0[k][1], w0 * v0[k][2], w0 * v0[k][3]};
+  }
+  if (npc > 1) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const float w1 = weight(1, hh_of[k]);
+      o[k][0] += w1 * v1[k][0]; o[k][1] += w1 * v1[k][1];
+      o[k][2] += w1 * v1[k][2]; o[k][3] += w1 * v1[k][3];
     }
-    T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 4 * c4;
-    const i16x4 pk = {MfmaOps<T>::from_f32(o[0]), MfmaOps<T>::from_f32(o[1]),
-                      MfmaOps<T>::from_f32(o[2]), MfmaOps<T>::from_f32(o[3])};
+  }
+  for (int i = 2; i < npc; ++i) {
+    f32x4 v[PER];
+    piece(i, v);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const float wi = weight(i, hh_of[k]);
+      o[k][0] += wi * v[k][0]; o[k][1] += wi * v[k][1];
+      o[k][2] += wi * v[k][2]; o[k][3] += wi * v[k][3];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int hh = hh_of[k];
+    const int h = hbase + hh;
+    if (g0 + hh >= hn || h >= a.num_heads) continue;
+    T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 4 * c4_of[k];
+    const i16x4 pk = {MfmaOps<T>::from_f32(o[k][0]), MfmaOps<T>::from_f32(o[k][1]),
+                      MfmaOps<T>::from_f32(o[k][2]), MfmaOps<T>::from_f32(o[k][3])};
     *(i16x4*)orow = pk;
-    if (c4 == 0) a.lse[(size_t)tok * a.num_heads + h] = l;
+    if (c4_of[k] == 0) a.lse[(size_t)tok * a.num_heads + h] = lse_s[hh];
   }
 }
 
@@ -728,7 +783,9 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   if ((phases & 2) && a.num_fd > 0) {
-    hipLaunchKernelGGL((merge_kernel<512, T>), dim3(a.num_fd), dim3(256), 0, st, a);
+    const int groups = (a.m_base + MERGE_HPB - 1) / MERGE_HPB;  // head groups per task (upper bound)
+    hipLaunchKernelGGL((merge_kernel<512, T>), dim3(a.num_fd, groups), dim3(MERGE_THREADS), 0, st,
+                       a);
     return hipGetLastError();
   }
   return hipSuccess;
