@@ -14,7 +14,9 @@ break, transposed operand) fails it; ``test_checks_have_teeth`` plants such
 slips in oracle outputs and asserts the checks fire.
 """
 
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -26,8 +28,10 @@ from oracle.golden_ref import (attend_token, cmp_threshold, gather_paged_rows, m
                                one_shot_reference, resolve_topk_rows, sparse_attn_oracle,
                                window_range)
 
-SCORES = [1.0, 3.0, 2.0, 5.0, 4.0, 0.0]
-VALUES = [10.0, 20.0, 30.0, 40.0, 50.0, 60.0]
+KAT = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                  "online_softmax_docs_kat.json"), encoding="utf-8"))
+SCORES = KAT["scores"]
+VALUES = KAT["values"]
 
 
 def _kat_rows():
@@ -36,19 +40,14 @@ def _kat_rows():
 
 
 @pytest.mark.parametrize("tile", [3, 512])
-def test_docs_worked_example_without_sink(tile):
+@pytest.mark.parametrize("case", range(len(KAT["cases"])))
+def test_docs_worked_example(tile, case):
+    c = KAT["cases"][case]
     q = torch.tensor([[0.0, 1.0]])
-    out, lse = attend_token(q, [_kat_rows()], torch.tensor([float("-inf")]), 1.0, tile=tile)
-    assert abs(float(out[0, 0]) - 40.038) < 1e-3
-    assert abs(float(lse[0]) - 5.4563) < 2e-4  # doc rounds intermediates to 4 places
-
-
-@pytest.mark.parametrize("tile", [3, 512])
-def test_docs_worked_example_with_sink(tile):
-    q = torch.tensor([[0.0, 1.0]])
-    out, lse = attend_token(q, [_kat_rows()], torch.tensor([2.0]), 1.0, tile=tile)
-    assert abs(float(out[0, 0]) - 38.813) < 1e-3
-    assert abs(float(lse[0]) - 5.4873) < 2e-4
+    sink = float("-inf") if c["sink"] is None else c["sink"]
+    out, lse = attend_token(q, [_kat_rows()], torch.tensor([sink]), 1.0, tile=tile)
+    assert abs(float(out[0, 0]) - c["out"]) < KAT["tolerance"]["out"]
+    assert abs(float(lse[0]) - c["lse"]) < KAT["tolerance"]["lse"]
 
 
 def test_empty_row_set_gives_zero_and_sink_lse():
