@@ -42,7 +42,21 @@ def parse():
     ap.add_argument("--workload", default="mla_decode_b64_h128_k2048")
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="after the benchmark, run 5 plain device copies of MIB MiB (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return ap.parse_args()
+
+
+def measured_traffic(workload):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"attn_kernel_{workload}_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path, encoding="utf-8"):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def cpu_baseline(inputs, counts):
@@ -175,13 +189,22 @@ def main():
                   "events around each of K separate launches",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "algorithmic_bytes": int(nbytes),
+                     "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(nbytes),
                      "kernel": "sas::attn_kernel"},
         "peaks": {"hbm_GBps": HBM_PEAK_GBPS, "bf16_mfma_TFLOPs": BF16_PEAK_TFLOPS},
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(sets[0], counts)
     print(json.dumps(res), flush=True)
+    if args.calibrate_copy > 0:
+        n = args.calibrate_copy << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"calibration: 5 device copies of {n} bytes", file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":
