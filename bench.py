@@ -4,8 +4,8 @@
 Workload (default ``mla_decode_b64_h128_k2048``): B=64 sequences, one query
 row each, H=128 heads, d_qk=576 (512 latent + 64 rope), d_v=512, bf16 q and
 paged KV (block 64) ~ N(0,1)*0.5, ctx 32768, top-k 2048 rows per query, no
-sink; split-KV schedule + LSE merge. A "step" is one call (attention kernel +
-merge kernel) over one input set. Four independent input sets (own pool,
+sink; split-KV schedule + LSE merge kernel. A "step" is one call (attention
+kernel + merge kernel) over one input set. Four independent input sets (own pool,
 block tables, top-k sets, q) rotate so the 256 MB Infinity Cache cannot hold
 the gathered rows between calls. Inputs are resident in HBM and the schedule
 is precomputed before the timed region.
@@ -127,7 +127,7 @@ def main():
         api.launch(preps[i % len(preps)])
     torch.cuda.synchronize()
 
-    # timed region 1: K whole calls (attention + merge, one C-ABI launch each)
+    # timed region 1: K whole calls (one C-ABI launch each: attention + merge kernels)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -139,8 +139,8 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = e0.elapsed_time(e1) / k
 
-    # timed region 2: the attention kernel alone, HIP events around every launch
-    # (launched on torch's current stream, which the events record on)
+    # timed region 2: the attention kernel alone, then the merge kernel alone, HIP
+    # events around every launch (on torch's current stream, which the events record on)
     def per_launch(phases):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * k)]
         torch.cuda.synchronize()
@@ -185,8 +185,8 @@ def main():
                            "p90": round(srt[(9 * k) // 10] * 1e3, 2)},
         "merge_kernel_us": round(merge_avg * 1e3, 2),
         "host_wall_us_per_step": round(wall / k * 1e6, 2),
-        "timing": "value/ms_per_step: K whole calls between two events; attn/merge: "
-                  "events around each of K separate launches",
+        "timing": "value/ms_per_step: K whole calls between two events; attn_kernel_us and "
+                  "merge_kernel_us: events around each of K separate launches",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(nbytes),

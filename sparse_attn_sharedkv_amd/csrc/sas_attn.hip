@@ -716,10 +716,12 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
       float mx = sink;
       for (int i = 0; i < nst; ++i) mx = fmaxf(mx, lse_p[i][hh]);
       for (int i = nst; i < npc; ++i) mx = fmaxf(mx, wl[(size_t)(slot0 + i) * mb + hloc + hh]);
-      float tot = __expf(sink - mx);
-      for (int i = 0; i < nst; ++i) tot += __expf(lse_p[i][hh] - mx);
-      for (int i = nst; i < npc; ++i) tot += __expf(wl[(size_t)(slot0 + i) * mb + hloc + hh] - mx);
-      l = mx + __logf(tot);
+      if (mx != -INFINITY) {  // else no key and no sink: lse -inf, every weight 0
+        float tot = __expf(sink - mx);
+        for (int i = 0; i < nst; ++i) tot += __expf(lse_p[i][hh] - mx);
+        for (int i = nst; i < npc; ++i) tot += __expf(wl[(size_t)(slot0 + i) * mb + hloc + hh] - mx);
+        l = mx + __logf(tot);
+      }
     }
     lse_s[hh] = l;
     for (int i = 0; i < nst; ++i) {

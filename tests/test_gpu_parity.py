@@ -40,7 +40,7 @@ HAS_GPU = torch.cuda.is_available()
 requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
 
 if HAS_GPU:
-    from sparse_attn_sharedkv_amd import (sparse_attn_sharedkv, sparse_attn_sharedkv_metadata,
+    from sparse_attn_sharedkv_amd import (api, sparse_attn_sharedkv, sparse_attn_sharedkv_metadata,
                                           sparse_flash_mla)
     from sparse_attn_sharedkv_amd.metadata import config_row
 
@@ -237,3 +237,26 @@ def test_full_size_mla_decode_sampled_tokens():
         ex, _ = one_shot_reference(q[b, 0].cpu().double().numpy(), rows,
                                    kw["sinks"].cpu().double().numpy(), kw["softmax_scale"])
         check_vs_exact(out[b, 0].cpu(), ro, ex[:, :512])
+
+
+def _call_phases(kw, phases, **extra):
+    prep = api.prepare(**_dev(kw), **extra)
+    api.launch(prep, phases=phases)
+    torch.cuda.synchronize()
+    return prep.out.clone(), prep.lse.clone()
+
+
+@requires_gpu
+def test_split_item_without_sink_and_without_keys():
+    # sinks -inf (no sink) and a token whose index row is all -1: golden gives
+    # m = -inf, l = 1 -> out 0, lse -inf; every split piece of that token is empty
+    _say("split item with no sink and no keys")
+    kw = _reduced_workload("mla_decode_b64_h128_k2048", 2, seed=9)
+    kw["cmp_sparse_indices"][1] = -1
+    kw["sinks"] = torch.full_like(kw["sinks"], float("-inf"))
+    out, lse = _call_phases(kw, 0, core_num=256)
+    out = out.reshape(kw["q"].shape[:-1] + (512,))
+    lse = lse.reshape(kw["q"].shape[:-1])
+    assert torch.equal(out[1].float().cpu(), torch.zeros_like(out[1].float().cpu()))
+    assert torch.isneginf(lse[1]).all()
+    _check_benchmark_regime(out, lse, kw)
