@@ -174,9 +174,10 @@ def main():
         "config": {"workload": args.workload, "batch": w["B"], "s_q": w["S"], "heads": w["H"],
                    "d_qk": w["D"], "d_v": w["DV"], "topk": w["K"], "ctx": list(w["ctx"]),
                    "block_size": 64, "input_sets": len(preps), "tokens": counts["tokens"],
-                   "attended_rows": counts["rows"]},
+                   "attended_rows": counts["rows"], "layout_q": sets[0]["layout_q"],
+                   "kv_row_bytes": counts["row_bytes"]},
         "us_per_call": round(ms_step * 1e3, 2),
-        "gathered_kv_GBps_call": round(counts["rows"] * counts["d_qk"] * 2 / (ms_step * 1e-3)
+        "gathered_kv_GBps_call": round(counts["rows"] * counts["row_bytes"] / (ms_step * 1e-3)
                                        / 1e9, 1),
         "hbm_roofline_frac_call": round(nbytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
         "mfma_frac_call": round(flops / (ms_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),

@@ -17,6 +17,9 @@
  *                             maps onto the same entry point with metadata built by the host.
  *   sas_workspace_bytes    <- workspace_idx auto-allocation of the JIT (kernel.py:353-382): the
  *                             caller allocates the split-KV partial buffer instead.
+ *   sas_kv_fp8_append      <- no counterpart in the reference (its caches are bf16/fp16 only,
+ *                             api.py:51-56): writer of the fp8 cache-row format that
+ *                             SAS_KV_FP8_DS_MLA selects for sas_attention_launch.
  */
 #ifndef SAS_MI355X_H_
 #define SAS_MI355X_H_
@@ -83,6 +86,19 @@ int64_t sas_workspace_bytes(int num_partial_slots, int m_base, int head_dim_v);
 #define SAS_DTYPE_BF16 0
 #define SAS_DTYPE_FP16 1
 
+/* KV cache row formats (SasAttnArgs.kv_format)
+ * SAS_KV_NATIVE: a row is head_dim elements of `dtype`.
+ * SAS_KV_FP8_DS_MLA: a row is SAS_FP8_ROW_BYTES = 656 bytes, for head_dim 576, dtype bf16:
+ *   bytes [0, 512)   dims 0..511 as OCP fp8 e4m3 (e4m3fn: no infinities, 0x7F/0xFF NaN)
+ *   bytes [512, 528) four fp32 scales; scale t covers dims 128t..128t+127
+ *   bytes [528, 656) dims 512..575 (rope) as bf16
+ * The attention reads dim d < 512 as bf16_rne(fp32(e4m3[d]) * scale[d / 128]) (one fp32
+ * multiply, then round-to-nearest-even to bf16), i.e. exactly the bf16 cache that
+ * dequantization gives, and computes on it as on a native bf16 cache. */
+#define SAS_KV_NATIVE 0
+#define SAS_KV_FP8_DS_MLA 1
+#define SAS_FP8_ROW_BYTES 656
+
 typedef struct SasAttnArgs {
   /* inputs (device pointers) */
   const void* q;                 /* [total_tokens, num_heads, head_dim] dtype                 */
@@ -111,11 +127,25 @@ typedef struct SasAttnArgs {
   /* kernels to enqueue: bit 0 attention, bit 1 split-KV merge; 0 means both.
    * A caller may enqueue the two phases as separate calls (attention first). */
   int32_t phases;
+  /* row format of ori_kv and cmp_kv: SAS_KV_NATIVE or SAS_KV_FP8_DS_MLA */
+  int32_t kv_format;
 } SasAttnArgs;
 
 /* Launch the attention kernel and, when num_fd > 0, the split-KV merge kernel on
  * `stream` (a hipStream_t). Asynchronous; no allocation, no host synchronisation. */
 int sas_attention_launch(const SasAttnArgs* args, void* stream);
+
+/* Quantize-on-append into a SAS_KV_FP8_DS_MLA cache (no reference counterpart: the
+ * reference has no fp8 cache; this is the producer of the format above).
+ * src: [n, 576] bf16 rows (device); slot_mapping: [n] int32 flat row index into the pool
+ * (block * block_size + offset; a negative entry skips that row); cache: [cache_rows, 656]
+ * bytes (device). Per row and 128-dim block t: amax = max |x|, scale = amax / 448 in fp32
+ * (1 when amax is 0), e4m3[d] = rne_e4m3(clamp(x[d] / scale, -448, 448)) with an IEEE fp32
+ * division; the rope dims are copied. Rows with a non-finite value give unspecified bytes.
+ * Slots outside [0, cache_rows) are skipped. Asynchronous on `stream`; returns
+ * SAS_E_INVALID for a null pointer or n < 0. */
+int sas_kv_fp8_append(const void* src, const int32_t* slot_mapping, void* cache, int n,
+                      int64_t cache_rows, void* stream);
 
 /* Library version (major * 100 + minor). */
 int sas_version(void);

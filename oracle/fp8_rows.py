@@ -1,0 +1,149 @@
+"""CPU restatement of the fp8 cache rows (``kv_cache_dtype="fp8_ds_mla"``).
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): never imported by the
+product package.
+
+The reference has no fp8 cache (its caches are bf16/fp16, api.py:51-56), so
+this format has no reference code or golden vectors: everything here is
+pinned by the format's definition and by library routines instead (tests in
+``tests/test_fp8_oracle.py``):
+
+* ``E4M3``            decode table built from the OCP e4m3 bit layout (1 sign,
+                      4 exponent bits with bias 7, 3 mantissa bits, subnormals
+                      at exponent 0, S.1111.111 = NaN, no infinities); checked
+                      against ``torch.float8_e4m3fn`` for all 256 codes and
+                      against closed-form values (1.0, 448, 2^-9, 2^-6);
+* ``encode_e4m3``     round-to-nearest-even onto the finite e4m3 values,
+                      checked against ``torch``'s cast on every tie and on
+                      random values, and for idempotence on every code;
+* ``bf16_rne``        fp32 -> bf16 round-to-nearest-even by bit arithmetic,
+                      checked against ``torch``'s cast;
+* ``quantize_rows``   the writer: per 128-dim block scale = amax / 448 (fp32
+                      division), codes = encode(clamp(x / scale)); checked by
+                      the block maximum landing exactly on +-448 and by the
+                      dequantization error bound (half an e4m3 step);
+* ``dequantize_rows`` the attention's view of a row: bf16(fp32(e4m3) * scale)
+                      for the latent dims, rope copied. An fp8 cache attends
+                      exactly like the bf16 cache this function returns, so the
+                      attention oracle for fp8 caches is ``golden_ref`` on the
+                      dequantized pool.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+ROW_BYTES = 656
+LATENT = 512
+ROPE = 64
+BLOCK = 128
+SCALE_OFF = 512
+ROPE_OFF = 528
+E4M3_MAX = 448.0
+
+
+def _build_e4m3() -> np.ndarray:
+    vals = np.empty(256, dtype=np.float64)
+    for c in range(256):
+        sign = -1.0 if c & 0x80 else 1.0
+        e = (c >> 3) & 0xF
+        m = c & 0x7
+        if e == 0xF and m == 0x7:
+            vals[c] = np.nan
+        elif e == 0:
+            vals[c] = sign * m * 2.0 ** -9          # subnormal: m/8 * 2^(1-7)
+        else:
+            vals[c] = sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return vals
+
+
+E4M3 = _build_e4m3()                                  # code -> value (float64, exact)
+_POS_CODES = np.array([c for c in range(0x7F)], dtype=np.int64)   # 0x00..0x7E, finite, >= 0
+_POS_VALS = E4M3[_POS_CODES]                          # increasing
+
+
+def decode_e4m3(codes: np.ndarray) -> np.ndarray:
+    """e4m3 codes (uint8) -> float32 values (exact)."""
+    return E4M3[np.asarray(codes, dtype=np.uint8)].astype(np.float32)
+
+
+def encode_e4m3(x: np.ndarray) -> np.ndarray:
+    """float32 values with |x| <= 448 -> nearest e4m3 code, ties to the even mantissa."""
+    x = np.asarray(x, dtype=np.float32).astype(np.float64)
+    if np.any(np.abs(x) > E4M3_MAX) or np.any(np.isnan(x)):
+        raise ValueError("encode_e4m3 takes finite values in [-448, 448]")
+    a = np.abs(x)
+    hi = np.searchsorted(_POS_VALS, a, side="left")          # first value >= a
+    hi = np.minimum(hi, len(_POS_VALS) - 1)
+    lo = np.maximum(hi - 1, 0)
+    d_lo = a - _POS_VALS[lo]
+    d_hi = _POS_VALS[hi] - a
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & ((_POS_CODES[hi] & 1) == 0))
+    code = np.where(pick_hi, _POS_CODES[hi], _POS_CODES[lo])
+    code = np.where(a == _POS_VALS[hi], _POS_CODES[hi], code)
+    neg = np.signbit(x)
+    return (code | np.where(neg, 0x80, 0)).astype(np.uint8)
+
+
+def bf16_rne(x: np.ndarray) -> np.ndarray:
+    """float32 -> float32 holding the bf16 round-to-nearest-even of each value."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    out = (r & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+    return np.where(nan, np.float32(np.nan), out).astype(np.float32)
+
+
+def quantize_rows(rows) -> np.ndarray:
+    """``[n, 576]`` bf16 (torch) or float32 holding bf16 values -> ``[n, 656]`` uint8 rows."""
+    if isinstance(rows, torch.Tensor):
+        rows = rows.to(torch.float32).cpu().numpy()
+    x = np.asarray(rows, dtype=np.float32).reshape(-1, LATENT + ROPE)
+    n = x.shape[0]
+    out = np.zeros((n, ROW_BYTES), dtype=np.uint8)
+    lat = x[:, :LATENT].reshape(n, LATENT // BLOCK, BLOCK)
+    amax = np.abs(lat).max(axis=2)                                   # [n, 4], exact
+    scale = np.where(amax > 0, amax / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
+    v = (lat / scale[:, :, None]).astype(np.float32)                 # IEEE fp32 division
+    v = np.clip(v, np.float32(-E4M3_MAX), np.float32(E4M3_MAX))
+    out[:, :LATENT] = encode_e4m3(v.reshape(n, LATENT))
+    out[:, SCALE_OFF:ROPE_OFF] = scale.astype("<f4").view(np.uint8).reshape(n, 16)
+    rope = torch.from_numpy(np.ascontiguousarray(x[:, LATENT:])).to(torch.bfloat16)
+    out[:, ROPE_OFF:] = rope.view(torch.int16).numpy().astype("<i2").view(np.uint8).reshape(n, 128)
+    return out
+
+
+def dequantize_rows(raw) -> torch.Tensor:
+    """``[..., 656]`` uint8 rows -> ``[..., 576]`` bf16: bf16(fp32(e4m3) * scale) ++ rope."""
+    if isinstance(raw, torch.Tensor):
+        raw = raw.cpu().view(torch.uint8).numpy()
+    raw = np.ascontiguousarray(np.asarray(raw, dtype=np.uint8))
+    lead = raw.shape[:-1]
+    r = raw.reshape(-1, ROW_BYTES)
+    n = r.shape[0]
+    vals = decode_e4m3(r[:, :LATENT]).reshape(n, LATENT // BLOCK, BLOCK)
+    scale = np.ascontiguousarray(r[:, SCALE_OFF:ROPE_OFF]).view("<f4").reshape(n, 4)
+    lat = bf16_rne((vals * scale[:, :, None]).astype(np.float32)).reshape(n, LATENT)
+    rope_bits = np.ascontiguousarray(r[:, ROPE_OFF:]).view("<i2").reshape(n, ROPE)
+    rope = torch.from_numpy(rope_bits.astype(np.int16)).view(torch.bfloat16).to(torch.float32)
+    full = np.concatenate([lat, rope.numpy()], axis=1)
+    return torch.from_numpy(full).to(torch.bfloat16).reshape(*lead, LATENT + ROPE)
+
+
+def random_rows(n: int, gen: torch.Generator, scale_range=(1e-3, 1e-2)) -> np.ndarray:
+    """``[n, 656]`` valid fp8 rows drawn directly in the stored format.
+
+    Codes uniform over the finite e4m3 values (0x7F / 0xFF excluded), scales
+    uniform in ``scale_range``, rope ~ N(0, 1) * 0.5 in bf16.
+    """
+    codes = torch.randint(0, 254, (n, LATENT), generator=gen, dtype=torch.int32)
+    codes = codes + (codes >= 0x7F).to(torch.int32)                 # skip 0x7F
+    out = np.zeros((n, ROW_BYTES), dtype=np.uint8)
+    out[:, :LATENT] = codes.numpy().astype(np.uint8)
+    lo, hi = scale_range
+    sc = (torch.rand((n, 4), generator=gen, dtype=torch.float32) * (hi - lo) + lo).numpy()
+    out[:, SCALE_OFF:ROPE_OFF] = sc.astype("<f4").view(np.uint8).reshape(n, 16)
+    rope = (torch.randn((n, ROPE), generator=gen) * 0.5).to(torch.bfloat16)
+    out[:, ROPE_OFF:] = rope.view(torch.int16).numpy().astype("<i2").view(np.uint8).reshape(n, 128)
+    return out

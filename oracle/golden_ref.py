@@ -20,6 +20,9 @@ Follows ``golden.py`` (reference) function by function:
 * ``sparse_attn_exact``      the same driver with the float64 closed form per
                               token (no tiling, no rounding): the exact answer
                               both golden and the HIP path approximate
+* fp8 caches (656-byte rows, no reference counterpart): rows are gathered
+  raw and dequantized with ``fp8_rows.dequantize_rows``; everything after
+  is the bf16 math above
 * ``merge_partials``         the closed-form split-KV merge
                               lse = log(e^sink + Σ e^lse_i),
                               o = Σ e^(lse_i - lse) · o_i
@@ -228,10 +231,18 @@ def token_layout(layout_q: str, q_shape, cu_seqlens_q: Optional[torch.Tensor]):
     return b, s_max, prefix, lens
 
 
+def _is_fp8_pool(pool, kv_cache_dtype) -> bool:
+    return kv_cache_dtype == "fp8_ds_mla" or (
+        kv_cache_dtype in (None, "auto") and pool.dtype in (torch.uint8, torch.float8_e4m3fn))
+
+
 def token_rows(*, b: int, s: int, act_q: int, act_kv: int, ori_kv, ori_block_table,
                cmp_kv, cmp_block_table, cmp_idx_row, cmp_ratio, ori_win_left,
-               ori_win_right=0) -> Tuple[torch.Tensor, torch.Tensor]:
-    """The two row segments (window rows, compressed rows) one query attends."""
+               ori_win_right=0, kv_cache_dtype=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The two row segments (window rows, compressed rows) one query attends.
+
+    fp8 pools (656-byte rows) are gathered raw and returned dequantized to bf16.
+    """
     s_glob = causal_position(act_kv, act_q, s)
     lo, hi = window_range(s_glob, ori_win_left, ori_win_right)
     ori_rows = gather_paged_rows(ori_kv, ori_block_table, b, range(lo, hi))
@@ -243,6 +254,9 @@ def token_rows(*, b: int, s: int, act_q: int, act_kv: int, ori_kv, ori_block_tab
     else:
         cmp_rows = gather_paged_rows(cmp_kv, cmp_block_table, b,
                                      resolve_topk_rows(cmp_idx_row, act_kv, act_q, s, cmp_ratio))
+    if _is_fp8_pool(ori_kv, kv_cache_dtype):
+        from .fp8_rows import dequantize_rows
+        ori_rows, cmp_rows = dequantize_rows(ori_rows), dequantize_rows(cmp_rows)
     return ori_rows, cmp_rows
 
 
@@ -255,7 +269,8 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
                        cmp_ratio: Optional[int] = None, ori_win_left: int = 127,
                        ori_win_right: int = 0, layout_q: str = "TND",
                        head_dim_v: Optional[int] = None,
-                       tokens: Optional[Sequence[int]] = None):
+                       tokens: Optional[Sequence[int]] = None,
+                       kv_cache_dtype: Optional[str] = None):
     """Golden output of ``sparse_attn_sharedkv`` for the API's own tensors.
 
     Returns ``(out, lse)`` in the caller's layout (``[T, N1, Dv]``/``[T, N1]``
@@ -292,7 +307,8 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
                 ori_block_table=ori_block_table, cmp_kv=cmp_kv,
                 cmp_block_table=cmp_block_table,
                 cmp_idx_row=None if idx_flat is None else idx_flat[t, 0].tolist(),
-                cmp_ratio=cmp_ratio, ori_win_left=ori_win_left, ori_win_right=ori_win_right)
+                cmp_ratio=cmp_ratio, ori_win_left=ori_win_left, ori_win_right=ori_win_right,
+                kv_cache_dtype=kv_cache_dtype)
             o, l = attend_token(q_flat[t], [ori_rows, cmp_rows], sinks, softmax_scale, d_v=dv)
             out[t] = o
             lse[t] = l
@@ -304,7 +320,7 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
 def sparse_attn_exact(q: torch.Tensor, *, ori_kv, ori_block_table, seqused_kv, sinks,
                       softmax_scale, cmp_kv=None, cmp_block_table=None, cmp_sparse_indices=None,
                       cu_seqlens_q=None, cmp_ratio=None, ori_win_left=127, ori_win_right=0,
-                      layout_q="TND", head_dim_v=None, tokens=None):
+                      layout_q="TND", head_dim_v=None, tokens=None, kv_cache_dtype=None):
     """float64 closed-form outputs ``(out, lse)`` over the same rows as ``sparse_attn_oracle``.
 
     Flat ``[T, N1, Dv]`` / ``[T, N1]`` numpy arrays; tokens outside ``tokens``
@@ -336,7 +352,8 @@ def sparse_attn_exact(q: torch.Tensor, *, ori_kv, ori_block_table, seqused_kv, s
                 cmp_kv=None if cmp_kv is None else cmp_kv.cpu(),
                 cmp_block_table=None if cmp_block_table is None else cmp_block_table.cpu(),
                 cmp_idx_row=None if idx_flat is None else idx_flat[t, 0].tolist(),
-                cmp_ratio=cmp_ratio, ori_win_left=ori_win_left, ori_win_right=ori_win_right)
+                cmp_ratio=cmp_ratio, ori_win_left=ori_win_left, ori_win_right=ori_win_right,
+                kv_cache_dtype=kv_cache_dtype)
             rows = torch.cat([ori_rows, cmp_rows]).to(torch.float64).numpy()
             o, l = one_shot_reference(q_flat[t].to(torch.float64).numpy(), rows, snk,
                                       softmax_scale)

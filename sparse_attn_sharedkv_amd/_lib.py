@@ -26,6 +26,9 @@ META_MAGIC = 0x5A53A355
 SAS_OK = 0
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
+KV_NATIVE = 0
+KV_FP8_DS_MLA = 1
+FP8_ROW_BYTES = 656
 
 
 class SasAttnArgs(ctypes.Structure):
@@ -69,11 +72,12 @@ class SasAttnArgs(ctypes.Structure):
         ("s2_base", ctypes.c_int32),
         ("m_base", ctypes.c_int32),
         ("phases", ctypes.c_int32),
+        ("kv_format", ctypes.c_int32),
     ]
 
 
-EXPORTS = ("sas_metadata_build", "sas_workspace_bytes", "sas_attention_launch", "sas_version",
-           "sas_args_struct_size", "sas_last_error")
+EXPORTS = ("sas_metadata_build", "sas_workspace_bytes", "sas_attention_launch",
+           "sas_kv_fp8_append", "sas_version", "sas_args_struct_size", "sas_last_error")
 
 _lock = threading.Lock()
 _lib = None
@@ -99,6 +103,9 @@ def load() -> ctypes.CDLL:
         lib.sas_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.sas_attention_launch.restype = ctypes.c_int
         lib.sas_attention_launch.argtypes = [ctypes.POINTER(SasAttnArgs), ctypes.c_void_p]
+        lib.sas_kv_fp8_append.restype = ctypes.c_int
+        lib.sas_kv_fp8_append.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_int, ctypes.c_int64, ctypes.c_void_p]
         lib.sas_version.restype = ctypes.c_int
         lib.sas_args_struct_size.restype = ctypes.c_int
         lib.sas_last_error.restype = ctypes.c_char_p

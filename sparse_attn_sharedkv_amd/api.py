@@ -12,8 +12,9 @@ free reshape). The paged caches go to the GPU untouched; the HIP kernels
 resolve block tables on the device. Additions over the reference, all
 optional and defaulting to its behaviour: ``head_dim_v`` (output width; the
 first ``head_dim_v`` columns of each shared row are V, as in MLA where
-d_qk = 576 and d_v = 512), and head counts other than 64 (multiples of 16 up
-to 128).
+d_qk = 576 and d_v = 512), head counts other than 64 (multiples of 16 up
+to 128), and ``kv_cache_dtype`` (``"fp8_ds_mla"``: 656-byte fp8 rows, see
+``kv_fp8``; by default inferred from the cache tensor's dtype).
 
 Errors follow the reference: AssertionError for unsupported masks / layouts,
 missing ``cu_seqlens_q`` in TND, top-k length mismatch and metadata size;
@@ -37,6 +38,17 @@ from .metadata import (DEFAULT_CORE_NUM, SAS_META_SIZE, build_metadata, config_r
 DEFAULT_BLOCK_I = 128  # kernel.py:65, kept for callers that import it
 SUPPORTED_HEAD_DIMS = (512, 576)
 SUPPORTED_HEAD_DIM_V = (512,)
+FP8_CACHE_DTYPES = (torch.uint8, torch.float8_e4m3fn)
+
+
+def _kv_format(kv_cache_dtype: Optional[str], ori_kv: torch.Tensor) -> int:
+    """Row format of the caches: native (q's dtype) or the 656-byte fp8 rows."""
+    if kv_cache_dtype in (None, "auto"):
+        return _lib.KV_FP8_DS_MLA if ori_kv.dtype in FP8_CACHE_DTYPES else _lib.KV_NATIVE
+    if kv_cache_dtype == "fp8_ds_mla":
+        return _lib.KV_FP8_DS_MLA
+    raise ValueError(f"unsupported kv_cache_dtype {kv_cache_dtype!r} "
+                     "(None, 'auto' or 'fp8_ds_mla')")
 
 
 def _dtype_code(t: torch.dtype) -> int:
@@ -82,7 +94,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             cmp_mask_mode: int = 3, ori_win_left: int = 127, ori_win_right: int = 0,
             layout_q: str = "TND", layout_kv: str = "PA_ND",
             core_num: int = DEFAULT_CORE_NUM, topk_cmp: Optional[int] = None,
-            head_dim_v: Optional[int] = None) -> Prepared:
+            head_dim_v: Optional[int] = None,
+            kv_cache_dtype: Optional[str] = None) -> Prepared:
     """Validate and stage one call (host work of api.py:186-384) without launching."""
     del seqused_q  # API-parity placeholder (api.py:186)
     assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
@@ -141,8 +154,11 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     else:
         n2 = ori_kv.shape[2]
 
-    dv = d if head_dim_v is None else int(head_dim_v)
-    if n2 != 1 or ori_kv.shape[2] != 1 or ori_kv.shape[-1] != d:
+    kv_fmt = _kv_format(kv_cache_dtype, ori_kv)
+    fp8 = kv_fmt == _lib.KV_FP8_DS_MLA
+    row_width = _lib.FP8_ROW_BYTES if fp8 else d
+    dv = (512 if fp8 else d) if head_dim_v is None else int(head_dim_v)
+    if n2 != 1 or ori_kv.shape[2] != 1 or ori_kv.shape[-1] != row_width:
         raise ValueError(f"only N2=1 shared KV with KV width == q width supported "
                          f"(got N2={n2}, q D={d}, kv {tuple(ori_kv.shape)})")
     if d not in SUPPORTED_HEAD_DIMS or dv not in SUPPORTED_HEAD_DIM_V or dv > d:
@@ -150,7 +166,14 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                          f"{SUPPORTED_HEAD_DIM_V} (got D={d}, head_dim_v={dv})")
     if n1 < 16 or n1 > 128 or n1 % 16 != 0:
         raise ValueError(f"N1 must be a multiple of 16 in [16, 128] (got N1={n1})")
-    if ori_kv.dtype != dtype or (cmp_kv is not None and cmp_kv.dtype != dtype):
+    if fp8:
+        if d != 576 or dtype != torch.bfloat16:
+            raise ValueError("fp8_ds_mla caches need bf16 queries with D=576")
+        for t in (ori_kv, cmp_kv):
+            if t is not None and t.dtype not in FP8_CACHE_DTYPES:
+                raise ValueError("fp8_ds_mla caches are uint8 or float8_e4m3fn tensors "
+                                 f"[blocks, block_size, 1, {_lib.FP8_ROW_BYTES}]")
+    elif ori_kv.dtype != dtype or (cmp_kv is not None and cmp_kv.dtype != dtype):
         raise ValueError("KV caches must have q's dtype")
     if ori_win_left < -1:
         raise ValueError("ori_win_left must be >= -1")
@@ -159,7 +182,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             raise ValueError("cmp_block_table is required with cmp_kv")
         if cmp_ratio is not None and cmp_ratio < 1:
             raise ValueError("cmp_ratio must be >= 1")
-        if cmp_kv.shape[-1] != d or cmp_kv.shape[2] != 1:
+        if cmp_kv.shape[-1] != row_width or cmp_kv.shape[2] != 1:
             raise ValueError("cmp_kv must be [blocks, block_size, 1, D]")
     cmp_ratio_eff = int(cmp_ratio) if cmp_ratio is not None else 4  # api.py:287
     if metadata is not None:
@@ -225,6 +248,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     a.topk = int(k)
     a.scenario, a.cmp_ratio, a.ori_win_left, a.dtype = scenario, cmp_ratio_eff, ori_win_left, dcode
     a.softmax_scale = float(softmax_scale)
+    a.kv_format = kv_fmt
     a.num_fa, a.num_fd = cfg["num_fa"], cfg["num_fd"]
     a.num_partial_slots, a.s2_base, a.m_base = (
         cfg["num_partial_slots"], cfg["s2_base"], cfg["m_base"])
@@ -286,6 +310,7 @@ def sparse_attn_sharedkv(
     core_num: int = DEFAULT_CORE_NUM,
     topk_cmp: Optional[int] = None,
     head_dim_v: Optional[int] = None,
+    kv_cache_dtype: Optional[str] = None,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Sparse shared-KV attention forward; returns ``attention_out`` in q's layout.
 
@@ -302,6 +327,7 @@ def sparse_attn_sharedkv(
                    cmp_ratio=cmp_ratio, ori_mask_mode=ori_mask_mode,
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
-                   core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v)
+                   core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
+                   kv_cache_dtype=kv_cache_dtype)
     launch(prep)
     return finalize(prep, return_softmax_lse)

@@ -167,6 +167,32 @@ __device__ inline void lds_wait_group(i16x4 (&r)[8]) {
                : "memory");
 }
 
+// Cache rows that a tile holds but the softmax masks (tile tails, -1 and
+// out-of-range top-k ids) are read from this all-zero row instead of the
+// pool: their P is 0, and 0 * V is only 0 when V is finite, which an
+// unwritten pool row need not be. Large enough for every row format.
+__device__ __attribute__((aligned(256))) unsigned char g_zero_row[1152];
+
+// fp8 cache rows (SAS_KV_FP8_DS_MLA): eight e4m3 values (one 8-byte word) times
+// their block scale, each product rounded to bf16 (v_cvt_pk_f32_fp8 decodes OCP
+// e4m3 exactly; v_mul_f32 and v_cvt_pk_bf16_f32 round to nearest even).
+__device__ inline i16x8 fp8x8_dequant_bf16(uint2 v, float s) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const f32x2 f0 = __builtin_amdgcn_cvt_pk_f32_fp8(v.x, false);
+  const f32x2 f1 = __builtin_amdgcn_cvt_pk_f32_fp8(v.x, true);
+  const f32x2 f2 = __builtin_amdgcn_cvt_pk_f32_fp8(v.y, false);
+  const f32x2 f3 = __builtin_amdgcn_cvt_pk_f32_fp8(v.y, true);
+  const bf16x2 b0 = __builtin_convertvector((f32x2){f0[0] * s, f0[1] * s}, bf16x2);
+  const bf16x2 b1 = __builtin_convertvector((f32x2){f1[0] * s, f1[1] * s}, bf16x2);
+  const bf16x2 b2 = __builtin_convertvector((f32x2){f2[0] * s, f2[1] * s}, bf16x2);
+  const bf16x2 b3 = __builtin_convertvector((f32x2){f3[0] * s, f3[1] * s}, bf16x2);
+  typedef short s2 __attribute__((ext_vector_type(2)));
+  const s2 w0 = __builtin_bit_cast(s2, b0), w1 = __builtin_bit_cast(s2, b1);
+  const s2 w2 = __builtin_bit_cast(s2, b2), w3 = __builtin_bit_cast(s2, b3);
+  return (i16x8){w0[0], w0[1], w1[0], w1[1], w2[0], w2[1], w3[0], w3[1]};
+}
+
 // ---------------------------------------------------------------------------
 // Attention kernel
 // ---------------------------------------------------------------------------
@@ -185,14 +211,20 @@ __device__ inline void lds_wait_group(i16x4 (&r)[8]) {
 // next DMA) and barrier B (P written; this tile's successor has landed). A
 // rescale (some head's max grew by more than 2^8) is decided workgroup-wide
 // after B and costs one more barrier.
-template <int DQK, int DV, int NHG, typename T>
+// fp8 rows (KVF = SAS_KV_FP8_DS_MLA): the main dims are loaded into VGPRs,
+// dequantized to bf16 and written to the same LDS layout, so every read of a
+// stage is the same as for a bf16 cache. Tile it + 2 is converted while tile
+// it's P·V runs, and tile it + 3's loads are issued right after.
+template <int DQK, int DV, int NHG, typename T, int KVF>
 __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   constexpr int NQ = 4;                  // dims / dv quarters per head group
   constexpr int NW = NQ * NHG;           // waves per workgroup
   constexpr int MB = 32 * NHG;           // heads per item (m-block)
   constexpr int NT = 64 * NW;            // threads
   constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
-  constexpr int ROWB = DQK * 2;          // bytes per cache row in HBM
+  constexpr bool FP8 = KVF == SAS_KV_FP8_DS_MLA;
+  constexpr int ROWB = FP8 ? SAS_FP8_ROW_BYTES : DQK * 2;  // bytes per cache row in HBM
+  constexpr int ROPE_OFF = FP8 ? 528 : 1024;               // byte offset of the rope dims
   constexpr int NKS_MAIN = 8;            // k-steps over 128 main dims
   constexpr int NKS = NKS_MAIN + (ROPE ? 1 : 0);
   constexpr int DVB = DV / 32 / NQ;      // 32-wide dv blocks per wave (4)
@@ -206,6 +238,9 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   static_assert(TILE % NW == 0, "rows per wave");
   static_assert(DVB == 4, "two groups of four dv blocks per wave");
   static_assert(NROPE <= NW, "at most one rope DMA instruction per wave");
+  static_assert(!FP8 || (ROPE && __is_same(T, __bf16)), "fp8 rows: head_dim 576, bf16");
+  constexpr int RPL = 2 * ROWS_PER_WAVE;  // fp8 path: rope bytes per lane per tile (8 or 16)
+  typedef uint32_t ropev __attribute__((ext_vector_type(RPL / 4)));
   typedef MfmaOps<T> Ops;
 
   __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTAGE * STAGE_BYTES];
@@ -382,8 +417,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
             id = (uint32_t)(phys * a.cmp_block_size + cid[e] % a.cmp_block_size) | 0x80000000u;
           }
         }
-        // masked rows still get a DMA: point them at row 0 of the original cache
-        rowid[r] = id == ROW_INVALID ? 0u : id;
+        rowid[r] = id;  // masked rows are read from the zero row
         const unsigned long long bal = __ballot(id != ROW_INVALID);
         if (lane == 0) {
           tmask[(r - lane) / TILE] = (uint32_t)bal;
@@ -398,7 +432,8 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       // branch-free row address (bit 31 of the id selects the compressed cache)
       auto row_ptr = [&](uint32_t id) -> const char* {
         const char* base = (id & 0x80000000u) ? cmp_kv : ori_kv;
-        return base + (size_t)(id & 0x7FFFFFFFu) * ROWB;
+        const char* p = base + (size_t)(id & 0x7FFFFFFFu) * ROWB;
+        return id == ROW_INVALID ? (const char*)g_zero_row : p;
       };
       // row ids a wave needs to issue one tile: lane j < ROWS_PER_WAVE holds the
       // id of its j-th main row; for the rope instruction (waves w < NROPE) lane
@@ -424,6 +459,40 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           dma16_vaddr(src, sbase + MAIN_BYTES + w * 1024);
         }
       };
+      // ---- fp8 rows: VGPR loads, then dequantize into one ring stage ----
+      // wave w takes rows w + NW j (j < ROWS_PER_WAVE): lane l loads bytes 8l..8l+7
+      // (dims 8l..8l+7, scale l / 16) of each, and RPL rope bytes of row
+      // w + NW (l / (128 / RPL)).
+      struct Fp8Tile {
+        uint2 v[ROWS_PER_WAVE];
+        float s[ROWS_PER_WAVE];
+        ropev rope;
+      };
+      constexpr int ROPE_LPR = 128 / RPL;  // lanes per row for the rope bytes
+      auto fp8_load = [&](Fp8Tile& f, uint32_t my_ids) {
+        const char* rp = nullptr;
+#pragma unroll
+        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
+          const char* p = row_ptr(__builtin_amdgcn_readlane(my_ids, j));
+          f.v[j] = *(const uint2*)(p + 8 * lane);
+          f.s[j] = *(const float*)(p + 512 + 4 * (lane >> 4));
+          rp = (lane / ROPE_LPR == j) ? p : rp;
+        }
+        f.rope = *(const ropev*)(rp + ROPE_OFF + (lane % ROPE_LPR) * RPL);
+      };
+      auto fp8_store = [&](const Fp8Tile& f, int stage) {
+        unsigned char* sb = kv_lds + stage * STAGE_BYTES;
+#pragma unroll
+        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
+          const int r = w + NW * j;
+          *(i16x8*)(sb + main_row_base(r) + 16 * lane) = fp8x8_dequant_bf16(f.v[j], f.s[j]);
+        }
+        const int r = w + NW * (lane / ROPE_LPR);
+        const int byte = (lane % ROPE_LPR) * RPL;
+        *(ropev*)(sb + MAIN_BYTES + rope_slot(r, byte >> 4) * 16 + (byte & 15)) = f.rope;
+      };
+      Fp8Tile fpt;
+
       // waits until at most the next tile's DMA instructions of this wave are in flight
       auto wait_tile = [&](bool next_in_flight) {
         if (!next_in_flight) {
@@ -437,8 +506,16 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         }
       };
 
-      issue(0, main_ids(0), rope_ids(0));
-      if (ntile > 1) issue(1, main_ids(1), rope_ids(1));
+      if constexpr (FP8) {
+        Fp8Tile f1;
+        fp8_load(fpt, main_ids(0));
+        if (ntile > 1) fp8_load(f1, main_ids(1));
+        fp8_store(fpt, 0);
+        if (ntile > 1) fp8_store(f1, 1);
+      } else {
+        issue(0, main_ids(0), rope_ids(0));
+        if (ntile > 1) issue(1, main_ids(1), rope_ids(1));
+      }
       if (c0 == p_lo) {
         const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
                                                  (head_ok ? head : 0)) * DQK;
@@ -453,6 +530,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       // puts no vmcnt wait for qf inside the tile loop (that wait would also drain
       // the row DMAs in flight on every tile). Also lands tiles 0 and 1.
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+      if (FP8 && ntile > 2) fp8_load(fpt, main_ids(2));
       __syncthreads();
 
       for (int it = 0; it < ntile; ++it) {
@@ -461,8 +539,9 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         // LDS words needed later in this tile, read now (latency hidden by Q·Kᵀ)
         const bool more = it + 2 < ntile;
         const uint32_t vm_tile = tmask[it];
-        const uint32_t nx_main = main_ids(more ? it + 2 : it);
-        const uint32_t nx_rope = rope_ids(more ? it + 2 : it);
+        const int nx_tile = FP8 ? (it + 3 < ntile ? it + 3 : it) : (more ? it + 2 : it);
+        const uint32_t nx_main = main_ids(nx_tile);
+        const uint32_t nx_rope = FP8 ? 0u : rope_ids(nx_tile);
         // ---- Sᵀ partial over this wave's dims quarter (K operands 3 deep) ----
         f32x16 st;
 #pragma unroll
@@ -487,7 +566,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         for (int G = 0; G < NQ; ++G)
           xpart[hg][G][q][lane] = (f32x4){st[4 * G], st[4 * G + 1], st[4 * G + 2], st[4 * G + 3]};
         __syncthreads();  // barrier A
-        if (more) issue((it + 2) % NSTAGE, nx_main, nx_rope);
+        if (!FP8 && more) issue((it + 2) % NSTAGE, nx_main, nx_rope);
 
         // fixed summation order over source quarters 0, 1, 2, 3
         const f32x4 sred = ((xpart[hg][q][0][lane] + xpart[hg][q][1][lane]) +
@@ -517,7 +596,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           *(i16x4*)(prow + pwr_off) = pk4;
         };
         make_p();
-        wait_tile(more);  // this wave's share of tile it + 1 has landed
+        if (!FP8) wait_tile(more);  // this wave's share of tile it + 1 has landed
         __syncthreads();  // barrier B
 
         // P operand of both k-steps and the rescale votes, in one round trip
@@ -582,6 +661,11 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           static_assert(NG == 2, "two k-steps per 32-row tile");
 #undef SAS_TR_GROUP
 #undef SAS_TR_MMA
+        }
+        // fp8 rows: stage (it + 2) % 3 last held tile it - 1, read before barrier A
+        if constexpr (FP8) {
+          if (more) fp8_store(fpt, (it + 2) % NSTAGE);
+          if (it + 3 < ntile) fp8_load(fpt, nx_main);
         }
       }
       __syncthreads();  // rowid / tmask / ring are rewritten by the next chunk or item
@@ -774,13 +858,13 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
   }
 }
 
-template <int DQK, int NHG, typename T>
+template <int DQK, int NHG, typename T, int KVF>
 static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   const int phases = a.phases == 0 ? 3 : a.phases;
   if (phases & 1) {
     const int per_xcd = (a.num_fa + 7) / 8;
-    hipLaunchKernelGGL((attn_kernel<DQK, 512, NHG, T>), dim3(8 * per_xcd), dim3(256 * NHG), 0,
-                       st, a);
+    hipLaunchKernelGGL((attn_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd), dim3(256 * NHG),
+                       0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -797,9 +881,17 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
 // dims-quarter waves): 4 or 8 waves, one or two per SIMD.
 template <typename T>
 static hipError_t dispatch_heads(const SasAttnArgs& a, hipStream_t st) {
+  constexpr int NAT = SAS_KV_NATIVE;
   if (a.head_dim == 576)
-    return a.m_base == 32 ? launch_attn<576, 1, T>(a, st) : launch_attn<576, 2, T>(a, st);
-  return a.m_base == 32 ? launch_attn<512, 1, T>(a, st) : launch_attn<512, 2, T>(a, st);
+    return a.m_base == 32 ? launch_attn<576, 1, T, NAT>(a, st) : launch_attn<576, 2, T, NAT>(a, st);
+  return a.m_base == 32 ? launch_attn<512, 1, T, NAT>(a, st) : launch_attn<512, 2, T, NAT>(a, st);
+}
+
+// fp8 rows: head_dim 576, bf16 queries and outputs
+static hipError_t dispatch_fp8(const SasAttnArgs& a, hipStream_t st) {
+  constexpr int F8 = SAS_KV_FP8_DS_MLA;
+  return a.m_base == 32 ? launch_attn<576, 1, __bf16, F8>(a, st)
+                        : launch_attn<576, 2, __bf16, F8>(a, st);
 }
 
 }  // namespace sas
@@ -859,10 +951,19 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     set_error("sas_attention_launch: more than 2^31 cache rows");
     return SAS_E_UNSUPPORTED;
   }
+  if (a->kv_format != SAS_KV_NATIVE && a->kv_format != SAS_KV_FP8_DS_MLA) {
+    set_error("sas_attention_launch: unknown kv_format");
+    return SAS_E_INVALID;
+  }
+  if (a->kv_format == SAS_KV_FP8_DS_MLA && (a->head_dim != 576 || a->dtype != SAS_DTYPE_BF16)) {
+    set_error("sas_attention_launch: fp8 cache rows need head_dim 576 and bf16 queries");
+    return SAS_E_UNSUPPORTED;
+  }
   if (a->batch == 0 || a->total_tokens == 0) return SAS_OK;
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e = a->dtype == SAS_DTYPE_FP16 ? sas::dispatch_heads<_Float16>(*a, st)
-                                            : sas::dispatch_heads<__bf16>(*a, st);
+  hipError_t e = a->kv_format == SAS_KV_FP8_DS_MLA ? sas::dispatch_fp8(*a, st)
+                 : a->dtype == SAS_DTYPE_FP16      ? sas::dispatch_heads<_Float16>(*a, st)
+                                                   : sas::dispatch_heads<__bf16>(*a, st);
   if (e != hipSuccess) {
     set_error(std::string("sas_attention_launch: ") + hipGetErrorString(e));
     return SAS_E_HIP;
@@ -870,7 +971,7 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
   return SAS_OK;
 }
 
-extern "C" int sas_version(void) { return 100; }
+extern "C" int sas_version(void) { return 110; }
 
 extern "C" int sas_args_struct_size(void) { return (int)sizeof(SasAttnArgs); }
 

@@ -41,6 +41,7 @@ def sparse_flash_mla(
     core_num: int = DEFAULT_CORE_NUM,
     topk_cmp: Optional[int] = None,
     head_dim_v: Optional[int] = 512,
+    kv_cache_dtype: Optional[str] = None,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Sparse flash-MLA forward: ``attention_out`` (and lse) in q's layout."""
     prep = prepare(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
@@ -50,6 +51,7 @@ def sparse_flash_mla(
                    cmp_ratio=cmp_ratio, ori_mask_mode=ori_mask_mode,
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
-                   core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v)
+                   core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
+                   kv_cache_dtype=kv_cache_dtype)
     launch(prep)
     return finalize(prep, return_softmax_lse)

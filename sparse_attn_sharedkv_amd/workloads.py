@@ -9,6 +9,11 @@ Shapes (BSND, block_size 64, q and KV ~ N(0, 1) * 0.5, softmax_scale = 1/sqrt(d_
 * ``mla_decode_b64_h128_k2048``      DeepSeek-V3.2 sparse MLA decode: B=64, H=128,
                                      ctx 32768, top-k 2048, no sink
 * ``mla_mtp_decode_b64_h128_k2048``  the same with two query rows per sequence (MTP)
+* ``mla_fp8_decode_t128_h128_k2048`` long-context sparse MLA over an fp8 cache: TND,
+                                     128 sequences of one query row, H=128, ctx
+                                     U[32768, 131072], top-k 2048, no sink; KV rows
+                                     N(0, 1) * 0.5 quantized into 656-byte fp8 rows
+                                     (``kv_fp8``)
 
 d_qk = 576 (512 latent + 64 rope), d_v = 512 throughout. Pure top-k attention
 is expressed through the reference API as a compressed cache equal to the raw
@@ -40,7 +45,13 @@ WORKLOADS: Dict[str, dict] = {
     "mla_mtp_decode_b64_h128_k2048": dict(B=64, S=2, H=128, D=576, DV=512, ctx=(32768, 32768),
                                           K=2048, window=-1, cmp_ratio=1, mode="topk",
                                           sinks="none"),
+    "mla_fp8_decode_t128_h128_k2048": dict(B=128, S=1, H=128, D=576, DV=512,
+                                           ctx=(32768, 131072), K=2048, window=-1, cmp_ratio=1,
+                                           mode="topk", sinks="none", kv="fp8_ds_mla",
+                                           layout="TND"),
 }
+
+FP8_POOL_CHUNK_ROWS = 1 << 20  # bf16 rows generated (then quantized) at a time
 
 
 def _pool(lens, block_size, d, dtype, rng, gen, device):
@@ -53,6 +64,28 @@ def _pool(lens, block_size, d, dtype, rng, gen, device):
         table[b, :nb] = phys[cur:cur + nb]
         cur += nb
     pool = (torch.randn((nblk, block_size, 1, d), generator=gen, device=device) * 0.5).to(dtype)
+    return pool, torch.as_tensor(table, dtype=torch.int32, device=device)
+
+
+def _pool_fp8(lens, block_size, rng, gen, device):
+    """fp8 pool: rows N(0, 1) * 0.5 in bf16, quantized chunk by chunk with the writer."""
+    from .kv_fp8 import ROW_BYTES, append_kv_fp8
+
+    per_b = [math.ceil(x / block_size) for x in lens]
+    nblk = max(sum(per_b), 1)
+    phys = rng.permutation(nblk).astype(np.int32)
+    table = np.full((len(lens), max(max(per_b), 1)), -1, dtype=np.int32)
+    cur = 0
+    for b, nb in enumerate(per_b):
+        table[b, :nb] = phys[cur:cur + nb]
+        cur += nb
+    pool = torch.empty((nblk, block_size, 1, ROW_BYTES), dtype=torch.uint8, device=device)
+    rows = nblk * block_size
+    for r0 in range(0, rows, FP8_POOL_CHUNK_ROWS):
+        n = min(FP8_POOL_CHUNK_ROWS, rows - r0)
+        src = (torch.randn((n, 576), generator=gen, device=device) * 0.5).to(torch.bfloat16)
+        slots = torch.arange(r0, r0 + n, dtype=torch.int32, device=device)
+        append_kv_fp8(pool, src, slots)
     return pool, torch.as_tensor(table, dtype=torch.int32, device=device)
 
 
@@ -79,7 +112,11 @@ def build_workload(name: str, *, device="cuda", seed: int = 0, batch: Optional[i
     q = (torch.randn((b, s_q, h, d), generator=gen(0), device=dev) * 0.5).to(dtype)
     kvg = gen(1)
     rng = np.random.default_rng(seed * 16 + 2)
-    ori_kv, ori_bt = _pool(lens, block_size, d, dtype, rng, kvg, dev)
+    fp8 = w.get("kv") == "fp8_ds_mla"
+    if fp8:
+        ori_kv, ori_bt = _pool_fp8(lens, block_size, rng, kvg, dev)
+    else:
+        ori_kv, ori_bt = _pool(lens, block_size, d, dtype, rng, kvg, dev)
     cmp_kv = cmp_bt = None
     if w["mode"] == "topk":
         cmp_kv, cmp_bt = ori_kv, ori_bt
@@ -101,20 +138,35 @@ def build_workload(name: str, *, device="cuda", seed: int = 0, batch: Optional[i
         sinks = torch.full((h,), float("-inf"), dtype=torch.float32, device=dev)
     else:
         sinks = (torch.rand((h,), generator=gen(5), device=dev) * 2 - 1).to(torch.float32)
-    return dict(q=q, ori_kv=ori_kv, ori_block_table=ori_bt, cmp_kv=cmp_kv,
+    args = dict(q=q, ori_kv=ori_kv, ori_block_table=ori_bt, cmp_kv=cmp_kv,
                 cmp_block_table=cmp_bt, cmp_sparse_indices=idx,
                 seqused_kv=torch.tensor(lens, dtype=torch.int32, device=dev), sinks=sinks,
                 softmax_scale=1.0 / math.sqrt(d), cmp_ratio=w["cmp_ratio"],
                 ori_win_left=w["window"], layout_q="BSND", head_dim_v=dv,
                 topk_cmp=k if k > 0 else None)
+    if fp8:
+        args["kv_cache_dtype"] = "fp8_ds_mla"
+    if w.get("layout") == "TND":
+        # varlen tokens: sequence i owns flat tokens [i * s_q, (i + 1) * s_q)
+        args["q"] = q.reshape(b * s_q, h, d)
+        args["cu_seqlens_q"] = torch.arange(0, b * s_q + 1, s_q, dtype=torch.int32, device=dev)
+        if idx is not None:
+            args["cmp_sparse_indices"] = idx.reshape(b * s_q, 1, k)
+        args["layout_q"] = "TND"
+    return args
 
 
 def workload_counts(args: dict) -> dict:
     """Query tokens, attended rows and top-k width of one input set."""
     q = args["q"]
-    b, s_q, h, d = q.shape
-    dv = args.get("head_dim_v") or d
     lens = [int(x) for x in args["seqused_kv"].cpu().tolist()]
+    if args.get("layout_q") == "TND":
+        t_n, h, d = q.shape
+        b = len(lens)
+        s_q = t_n // max(b, 1)
+    else:
+        b, s_q, h, d = q.shape
+    dv = args.get("head_dim_v") or d
     win = args["ori_win_left"]
     idx = args["cmp_sparse_indices"]
     valid = None
@@ -127,8 +179,9 @@ def workload_counts(args: dict) -> dict:
             rows += max(0, sg + 1 - max(sg - win, 0))
             if valid is not None:
                 rows += int(valid[bi * s_q + s])
+    fp8 = args.get("kv_cache_dtype") == "fp8_ds_mla"
     return dict(tokens=b * s_q, rows=rows, heads=h, d_qk=d, d_v=dv,
-                k=idx.shape[-1] if idx is not None else 0)
+                k=idx.shape[-1] if idx is not None else 0, row_bytes=656 if fp8 else 2 * d)
 
 
 def flops_and_bytes(counts: dict, kv_row_bytes: Optional[int] = None) -> tuple:
@@ -140,7 +193,7 @@ def flops_and_bytes(counts: dict, kv_row_bytes: Optional[int] = None) -> tuple:
     """
     t, rows, h = counts["tokens"], counts["rows"], counts["heads"]
     dq, dv, k = counts["d_qk"], counts["d_v"], counts["k"]
-    rb = kv_row_bytes if kv_row_bytes is not None else dq * 2
+    rb = kv_row_bytes if kv_row_bytes is not None else counts.get("row_bytes", dq * 2)
     flops = 2.0 * rows * h * (dq + dv)
     nbytes = rows * rb + t * h * dq * 2 + t * h * dv * 2 + t * h * 4 + t * k * 4 + rows * 4
     return flops, float(nbytes)

@@ -72,3 +72,36 @@ def test_no_cpu_path(swa_case, scfa_case):
         sparse_attn_sharedkv(**swa_case)
     with pytest.raises(RuntimeError):
         sparse_flash_mla(**{k: v for k, v in scfa_case.items()})
+
+
+def _fp8_call(**over):
+    q = torch.zeros(1, 64, 576, dtype=torch.bfloat16)
+    kv = torch.zeros(4, 64, 1, 656, dtype=torch.uint8)
+    tbl = torch.zeros(1, 4, dtype=torch.int32)
+    kw = dict(q=q, ori_kv=kv, ori_block_table=tbl, cmp_kv=kv, cmp_block_table=tbl,
+              cmp_sparse_indices=torch.zeros(1, 1, 8, dtype=torch.int32),
+              cu_seqlens_q=torch.tensor([0, 1], dtype=torch.int32),
+              seqused_kv=torch.tensor([100], dtype=torch.int32),
+              sinks=torch.zeros(64), softmax_scale=1 / 24, cmp_ratio=1, ori_win_left=-1)
+    kw.update(over)
+    return kw
+
+
+def test_fp8_cache_gates():
+    # well-formed fp8 call: passes validation, then has no CPU path
+    with pytest.raises(RuntimeError):
+        sparse_flash_mla(**_fp8_call())
+    with pytest.raises(RuntimeError):
+        sparse_flash_mla(**_fp8_call(), kv_cache_dtype="fp8_ds_mla")
+    with pytest.raises(ValueError):                      # unknown format name
+        sparse_flash_mla(**_fp8_call(), kv_cache_dtype="fp8_e5m2")
+    with pytest.raises(ValueError):                      # fp16 queries
+        sparse_flash_mla(**_fp8_call(q=torch.zeros(1, 64, 576, dtype=torch.float16)))
+    with pytest.raises(ValueError):                      # D = 512 queries
+        sparse_flash_mla(**_fp8_call(q=torch.zeros(1, 64, 512, dtype=torch.bfloat16)))
+    kv = torch.zeros(4, 64, 1, 576, dtype=torch.uint8)   # not 656-byte rows
+    with pytest.raises(ValueError):
+        sparse_flash_mla(**_fp8_call(ori_kv=kv, cmp_kv=kv))
+    kv = torch.zeros(4, 64, 1, 656, dtype=torch.bfloat16)  # bf16 tensor named fp8
+    with pytest.raises(ValueError):
+        sparse_flash_mla(**_fp8_call(ori_kv=kv, cmp_kv=kv), kv_cache_dtype="fp8_ds_mla")

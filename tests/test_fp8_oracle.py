@@ -1,0 +1,127 @@
+"""Pins of the fp8 cache-row oracle (``oracle/fp8_rows.py``) on the CPU.
+
+The reference has no fp8 cache, so nothing here comes from its tests: the
+format's definition (OCP e4m3 bit layout), closed-form values, torch's
+``float8_e4m3fn`` / ``bfloat16`` casts (library routines) and error bounds
+fix each function, chosen so that a wrong bias, a dropped subnormal, a
+round-half-up instead of half-even or a misplaced scale fails.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_rows as F
+
+
+def _torch_e4m3(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.float8_e4m3fn).view(
+        torch.uint8).numpy()
+
+
+def test_decode_table_matches_library_and_closed_forms():
+    lib = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    mine = F.decode_e4m3(np.arange(256, dtype=np.uint8))
+    assert np.array_equal(np.isnan(mine), np.isnan(lib))
+    fin = ~np.isnan(lib)
+    assert np.array_equal(mine[fin], lib[fin])
+    # closed forms: 1.0, the largest finite, smallest subnormal, smallest normal, -2
+    assert mine[0x38] == 1.0 and mine[0x7E] == 448.0 and mine[0xFE] == -448.0
+    assert mine[0x01] == 2.0 ** -9 and mine[0x08] == 2.0 ** -6 and mine[0xC0] == -2.0
+    assert np.isnan(mine[0x7F]) and np.isnan(mine[0xFF])
+    assert int(np.isnan(mine).sum()) == 2                  # e4m3fn: no infinities
+
+
+def test_encode_round_to_nearest_even_matches_library():
+    fin = np.unique(F.E4M3[~np.isnan(F.E4M3)]).astype(np.float32)
+    mids = ((fin[:-1].astype(np.float64) + fin[1:]) / 2).astype(np.float32)
+    up = np.nextafter(mids, np.float32(np.inf))
+    dn = np.nextafter(mids, np.float32(-np.inf))
+    rng = np.random.default_rng(0)
+    rnd = rng.uniform(-448, 448, 20000).astype(np.float32)
+    tiny = (rng.standard_normal(5000) * 2e-3).astype(np.float32)
+    x = np.concatenate([fin, mids, up, dn, rnd, tiny, np.float32([0.0, -0.0])])
+    x = x[np.abs(x) <= 448]
+    assert np.array_equal(F.encode_e4m3(x), _torch_e4m3(x))
+
+
+def test_encode_ties_go_to_even_and_codes_round_trip():
+    # 1 + 1/16 lies halfway between 1 (0x38, even) and 1.125 (0x39): even wins
+    assert F.encode_e4m3(np.float32([1.0625]))[0] == 0x38
+    # 1.1875 lies halfway between 1.125 (0x39, odd) and 1.25 (0x3A, even)
+    assert F.encode_e4m3(np.float32([1.1875]))[0] == 0x3A
+    # halfway between the largest subnormal (0x07) and the smallest normal (0x08)
+    assert F.encode_e4m3(np.float32([7.5 * 2 ** -9]))[0] == 0x08
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], dtype=np.uint8)
+    assert np.array_equal(F.encode_e4m3(F.decode_e4m3(codes)), codes)
+
+
+def test_bf16_rne_matches_library():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(50000).astype(np.float32) * np.float32(3.0)
+    bits = x.view(np.uint32)
+    ties = ((bits & 0xFFFF0000) | 0x8000).view(np.float32)       # exact halfway cases
+    y = np.concatenate([x, ties, np.float32([0.0, -0.0, 1e-40, 3.4e38])])
+    lib = torch.from_numpy(y).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(F.bf16_rne(y), lib)
+
+
+def test_quantize_known_block():
+    # amax 1 -> scale 1/448; 1 -> 448 (0x7E), -0.5 -> -224 (0xF6), 0.25 -> 112 (0x6E)
+    row = np.zeros((1, 576), np.float32)
+    row[0, :4] = [1.0, -0.5, 0.25, 0.0]
+    raw = F.quantize_rows(row)
+    assert list(raw[0, :4]) == [0x7E, 0xF6, 0x6E, 0x00]
+    scales = raw[0, 512:528].view("<f4")
+    assert scales[0] == np.float32(1.0) / np.float32(448.0)
+    assert list(scales[1:]) == [1.0, 1.0, 1.0]                    # all-zero blocks
+    assert not raw[0, 4:512].any()
+
+
+def test_quantize_block_max_hits_448_and_error_bound():
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn((64, 576), generator=g) * 0.5).to(torch.bfloat16)
+    x[3, 128:256] *= 1000.0                                      # one large block
+    x[5, :128] = 0.0                                             # one zero block
+    raw = F.quantize_rows(x)
+    xf = x.float().numpy()
+    codes = raw[:, :512].reshape(64, 4, 128)
+    lat = np.abs(xf[:, :512]).reshape(64, 4, 128)
+    for r in range(64):
+        for t in range(4):
+            if lat[r, t].max() > 0:
+                i = int(lat[r, t].argmax())
+                assert codes[r, t, i] in (0x7E, 0xFE)
+    deq = F.dequantize_rows(raw).float().numpy()
+    scale = raw[:, 512:528].copy().view("<f4").reshape(64, 4)
+    sc = np.repeat(scale, 128, axis=1)
+    # half an e4m3 step (|v|/16 for normals, 2^-10 below) times the scale, plus bf16 rounding
+    v = np.abs(xf[:, :512]) / sc
+    bound = np.maximum(v / 16, 2.0 ** -10) * sc * (1 + 2 ** -8) + np.abs(deq[:, :512]) * 2 ** -8
+    assert np.all(np.abs(deq[:, :512] - xf[:, :512]) <= bound)
+    assert np.array_equal(deq[:, 512:], xf[:, 512:])             # rope copied exactly
+    assert not deq[5, :128].any()
+
+
+def test_dequantize_is_fp32_product_rounded_to_bf16():
+    g = torch.Generator().manual_seed(3)
+    raw = F.random_rows(16, g)
+    deq = F.dequantize_rows(raw).float().numpy()
+    vals = torch.from_numpy(raw[:, :512].copy()).view(torch.float8_e4m3fn).float()
+    scale = torch.from_numpy(raw[:, 512:528].copy().view("<f4").reshape(16, 4))
+    want = (vals.reshape(16, 4, 128) * scale[:, :, None]).reshape(16, 512).to(torch.bfloat16)
+    assert np.array_equal(deq[:, :512], want.float().numpy())
+    assert not np.isnan(deq).any()
+
+
+def test_random_rows_are_valid():
+    raw = F.random_rows(256, torch.Generator().manual_seed(4))
+    assert not np.isin(raw[:, :512], [0x7F, 0xFF]).any()
+    sc = raw[:, 512:528].copy().view("<f4")
+    assert np.all((sc >= 1e-3) & (sc <= 1e-2))
+
+
+@pytest.mark.parametrize("bad", [449.0, float("nan")])
+def test_encode_rejects_out_of_range(bad):
+    with pytest.raises(ValueError):
+        F.encode_e4m3(np.float32([bad]))

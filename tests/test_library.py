@@ -20,7 +20,7 @@ HEADER = os.path.join(ROOT, "include", "sas_mi355x.h")
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(sas_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(sas_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -40,11 +40,21 @@ def test_struct_layout_matches_binding():
 
 def test_header_constants_match_binding():
     text = open(HEADER).read()
-    consts = dict(re.findall(r"#define (SAS_[A-Z_]+) (\S+)", text))
+    consts = dict(re.findall(r"#define (SAS_[A-Z0-9_]+) (\S+)", text))
     assert int(consts["SAS_AIC_CORE_NUM"]) == _lib.AIC_CORE_NUM
     assert int(consts["SAS_AIV_CORE_NUM"]) == _lib.AIV_CORE_NUM
     assert int(consts["SAS_META_SIZE"]) == _lib.SAS_META_SIZE
     assert int(consts["SAS_META_MAGIC"], 16) == _lib.META_MAGIC
+    assert int(consts["SAS_KV_NATIVE"]) == _lib.KV_NATIVE
+    assert int(consts["SAS_KV_FP8_DS_MLA"]) == _lib.KV_FP8_DS_MLA
+    assert int(consts["SAS_FP8_ROW_BYTES"]) == _lib.FP8_ROW_BYTES == 512 + 16 + 128
+
+
+def test_fp8_writer_rejects_bad_arguments_without_a_gpu():
+    lib = _lib.load()
+    assert lib.sas_kv_fp8_append(None, None, None, 4, 16, None) == -1
+    assert lib.sas_kv_fp8_append(None, None, None, -1, 16, None) == -1
+    assert lib.sas_kv_fp8_append(None, None, None, 0, 16, None) == 0   # nothing to do
 
 
 def test_workspace_bytes():
