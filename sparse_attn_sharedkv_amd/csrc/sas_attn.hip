@@ -141,6 +141,15 @@ __device__ inline void dma16_vaddr(const void* gptr, uint32_t lds_base) {
       : "memory");
 }
 
+// Materialise a value at this point of the program: the empty asm (ordered
+// with the barriers and the DMA asm) consumes it, so its computation cannot be
+// sunk past the next barrier towards its use.
+__device__ inline void pin_u64(uint64_t& v) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  v = ((uint64_t)hi << 32) | lo;
+}
+
 template <int N>
 __device__ inline void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -435,27 +444,36 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         const char* p = base + (size_t)(id & 0x7FFFFFFFu) * ROWB;
         return id == ROW_INVALID ? (const char*)g_zero_row : p;
       };
-      // row ids a wave needs to issue one tile: lane j < ROWS_PER_WAVE holds the
-      // id of its j-th main row; for the rope instruction (waves w < NROPE) lane
-      // l holds the id of row 8w + l/8. Read ahead of use to hide LDS latency.
-      auto main_ids = [&](int tile) -> uint32_t {
-        return rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)];
+      // row addresses a wave needs to issue one tile, computed per lane ahead of
+      // use (off the path between barrier A and the DMA issue): lane j <
+      // ROWS_PER_WAVE holds the address of its j-th main row; for the rope
+      // instruction (waves w < NROPE) lane l holds that of row 8w + l/8.
+      auto main_ptrs = [&](int tile) -> uint64_t {
+        return (uint64_t)(uintptr_t)row_ptr(
+            rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
       };
-      auto rope_ids = [&](int tile) -> uint32_t {
-        return ROPE && w < NROPE ? rowid[tile * TILE + 8 * w + (lane >> 3)] : 0u;
+      auto rope_ptr = [&](int tile) -> uint64_t {
+        return ROPE && w < NROPE
+                   ? (uint64_t)(uintptr_t)row_ptr(rowid[tile * TILE + 8 * w + (lane >> 3)])
+                   : (uint64_t)(uintptr_t)g_zero_row;
       };
-      auto issue = [&](int stage, uint32_t my_ids, uint32_t rope_id) {
+      // address of main row j from lane j (two v_readlane, no scalar arithmetic)
+      auto lane_row = [&](uint64_t ptrs, int j) -> const char* {
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ptrs, j);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(ptrs >> 32), j);
+        return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+      };
+      auto issue = [&](int stage, uint64_t my_ptrs, uint64_t rope_row) {
         const uint32_t sbase = kv_base + stage * STAGE_BYTES;
 #pragma unroll
         for (int j = 0; j < ROWS_PER_WAVE; ++j) {
           const int r = w + NW * j;
-          const uint32_t id = __builtin_amdgcn_readlane(my_ids, j);
-          dma16_sbase(row_ptr(id), (uint32_t)lane * 16u, sbase + main_row_base(r));
+          dma16_sbase(lane_row(my_ptrs, j), (uint32_t)lane * 16u, sbase + main_row_base(r));
         }
         if (ROPE && w < NROPE) {
           const int r = 8 * w + (lane >> 3);
           const int cr = ((lane & 7) - (r >> 1)) & 7;
-          const char* src = row_ptr(rope_id) + 1024 + cr * 16;
+          const char* src = (const char*)(uintptr_t)rope_row + 1024 + cr * 16;
           dma16_vaddr(src, sbase + MAIN_BYTES + w * 1024);
         }
       };
@@ -469,11 +487,11 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         ropev rope;
       };
       constexpr int ROPE_LPR = 128 / RPL;  // lanes per row for the rope bytes
-      auto fp8_load = [&](Fp8Tile& f, uint32_t my_ids) {
+      auto fp8_load = [&](Fp8Tile& f, uint64_t my_ptrs) {
         const char* rp = nullptr;
 #pragma unroll
         for (int j = 0; j < ROWS_PER_WAVE; ++j) {
-          const char* p = row_ptr(__builtin_amdgcn_readlane(my_ids, j));
+          const char* p = lane_row(my_ptrs, j);
           f.v[j] = *(const uint2*)(p + 8 * lane);
           f.s[j] = *(const float*)(p + 512 + 4 * (lane >> 4));
           rp = (lane / ROPE_LPR == j) ? p : rp;
@@ -508,13 +526,13 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
 
       if constexpr (FP8) {
         Fp8Tile f1;
-        fp8_load(fpt, main_ids(0));
-        if (ntile > 1) fp8_load(f1, main_ids(1));
+        fp8_load(fpt, main_ptrs(0));
+        if (ntile > 1) fp8_load(f1, main_ptrs(1));
         fp8_store(fpt, 0);
         if (ntile > 1) fp8_store(f1, 1);
       } else {
-        issue(0, main_ids(0), rope_ids(0));
-        if (ntile > 1) issue(1, main_ids(1), rope_ids(1));
+        issue(0, main_ptrs(0), rope_ptr(0));
+        if (ntile > 1) issue(1, main_ptrs(1), rope_ptr(1));
       }
       if (c0 == p_lo) {
         const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
@@ -530,7 +548,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       // puts no vmcnt wait for qf inside the tile loop (that wait would also drain
       // the row DMAs in flight on every tile). Also lands tiles 0 and 1.
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
-      if (FP8 && ntile > 2) fp8_load(fpt, main_ids(2));
+      if (FP8 && ntile > 2) fp8_load(fpt, main_ptrs(2));
       __syncthreads();
 
       for (int it = 0; it < ntile; ++it) {
@@ -540,8 +558,8 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         const bool more = it + 2 < ntile;
         const uint32_t vm_tile = tmask[it];
         const int nx_tile = FP8 ? (it + 3 < ntile ? it + 3 : it) : (more ? it + 2 : it);
-        const uint32_t nx_main = main_ids(nx_tile);
-        const uint32_t nx_rope = FP8 ? 0u : rope_ids(nx_tile);
+        uint64_t nx_main = main_ptrs(nx_tile);
+        uint64_t nx_rope = FP8 ? 0ull : rope_ptr(nx_tile);
         // ---- Sᵀ partial over this wave's dims quarter (K operands 3 deep) ----
         f32x16 st;
 #pragma unroll
@@ -561,6 +579,9 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
             st = Ops::mma(kop, qf[ks], st);
           }
         }
+        // next DMA addresses: computed while the Q·Kᵀ MFMAs drain
+        pin_u64(nx_main);
+        if (!FP8) pin_u64(nx_rope);
         // ---- reduce-scatter of the partials: quarter G's rows go to wave G ----
 #pragma unroll
         for (int G = 0; G < NQ; ++G)
