@@ -157,7 +157,7 @@ __device__ inline void wait_vmcnt() {
 
 // ds_read_b64_tr_b16 with an immediate offset (the builtin does not fold
 // offsets, which costs one address VGPR per read). The result is not tracked
-// by the compiler's lgkmcnt bookkeeping: consume it only after lds_wait_group.
+// by the compiler's lgkmcnt bookkeeping: consume it only after lds_wait_pv.
 template <int OFF>
 __device__ inline i16x4 ds_read_tr16(uint32_t addr) {
   i16x4 v;
@@ -165,14 +165,29 @@ __device__ inline i16x4 ds_read_tr16(uint32_t addr) {
   return v;
 }
 
-// Wait until at most N LDS operations are outstanding; the eight registers
-// pass through the asm so no consumer can be scheduled above the wait.
-template <int N>
-__device__ inline void lds_wait_group(i16x4 (&r)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(%8)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
-                 "+v"(r[6]), "+v"(r[7])
-               : "n"(N)
+template <int OFF>
+__device__ inline i16x8 ds_read_b128_asm(uint32_t addr) {
+  i16x8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+  return v;
+}
+__device__ inline uint64_t ds_read_b64_asm(uint32_t addr) {
+  uint64_t v;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Wait for every LDS operation of this wave; all registers written by the
+// untracked asm reads pass through the asm, so no consumer (and no copy) of
+// them can be placed above the wait.
+__device__ inline void lds_wait_pv(uint64_t& votes, i16x8 (&p)[2], i16x4 (&g0)[8],
+                                   i16x4 (&g1)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(votes), "+v"(p[0]), "+v"(p[1]), "+v"(g0[0]), "+v"(g0[1]), "+v"(g0[2]),
+                 "+v"(g0[3]), "+v"(g0[4]), "+v"(g0[5]), "+v"(g0[6]), "+v"(g0[7]), "+v"(g1[0]),
+                 "+v"(g1[1]), "+v"(g1[2]), "+v"(g1[3]), "+v"(g1[4]), "+v"(g1[5]), "+v"(g1[6]),
+                 "+v"(g1[7])
+               :
                : "memory");
 }
 
@@ -620,11 +635,32 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         if (!FP8) wait_tile(more);  // this wave's share of tile it + 1 has landed
         __syncthreads();  // barrier B
 
-        // P operand of both k-steps and the rescale votes, in one round trip
+        // rescale votes, P operand of both k-steps and Vᵀ of the whole tile:
+        // issued together, then one wait (none of the asm outputs is touched
+        // before it)
+        const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
+        const uint32_t pka = (uint32_t)(uintptr_t)(prow + 16 * hl);
+        uint64_t votes = ds_read_b64_asm((uint32_t)(uintptr_t)flags);
         i16x8 pk[2];
-        pk[0] = *(const i16x8*)(prow + 16 * hl);
-        pk[1] = *(const i16x8*)(prow + 32 + 16 * hl);
-        const uint64_t votes = *(const uint64_t*)flags;
+        pk[0] = ds_read_b128_asm<0>(pka);
+        pk[1] = ds_read_b128_asm<32>(pka);
+        i16x4 gbuf[2][8];
+#define SAS_TR_GROUP(GI, DST)                                                              \
+  {                                                                                        \
+    constexpr int q_ = (GI);                                                               \
+    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 0 * 64>(trb);                       \
+    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 0 * 64>(trb);              \
+    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 1 * 64>(trb);                       \
+    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 1 * 64>(trb);              \
+    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 2 * 64>(trb);                       \
+    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 2 * 64>(trb);              \
+    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 3 * 64>(trb);                       \
+    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 3 * 64>(trb);              \
+  }
+        SAS_TR_GROUP(0, gbuf[0]);
+        SAS_TR_GROUP(1, gbuf[1]);
+#undef SAS_TR_GROUP
+        lds_wait_pv(votes, pk, gbuf[0], gbuf[1]);
         if (__builtin_amdgcn_readfirstlane((uint32_t)(votes | (votes >> 32)))) {
           // rescale: every wave of the head group derives the same new max
           float mt = mbuf[hg][0][lane & 31];
@@ -648,41 +684,15 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         l_part += (pv[0] + pv[1]) + (pv[2] + pv[3]);
 
         // ---- Oᵀ += Vᵀ · Pᵀ over both 16-row k-steps ----
-        {
-          constexpr int NG = 2;  // groups: (k-step kq, dv blocks 0..3)
-          const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
-          i16x4 gbuf[2][8];
-#define SAS_TR_GROUP(GI, DST)                                                              \
-  {                                                                                        \
-    constexpr int q_ = (GI);                                                               \
-    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 0 * 64>(trb);                       \
-    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 0 * 64>(trb);              \
-    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 1 * 64>(trb);                       \
-    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 1 * 64>(trb);              \
-    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 2 * 64>(trb);                       \
-    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 2 * 64>(trb);              \
-    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 3 * 64>(trb);                       \
-    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 3 * 64>(trb);              \
-  }
-#define SAS_TR_MMA(GI, SRC)                                                                \
-  {                                                                                        \
-    _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                        \
-      const i16x8 aop = {SRC[2 * e][0],     SRC[2 * e][1],     SRC[2 * e][2],              \
-                         SRC[2 * e][3],     SRC[2 * e + 1][0], SRC[2 * e + 1][1],          \
-                         SRC[2 * e + 1][2], SRC[2 * e + 1][3]};                            \
-      acc[e] = Ops::mma(aop, pk[(GI)], acc[e]);                                            \
-    }                                                                                      \
-  }
-          SAS_TR_GROUP(0, gbuf[0]);
-          SAS_TR_GROUP(1, gbuf[1]);
-          lds_wait_group<8>(gbuf[0]);
-          SAS_TR_MMA(0, gbuf[0]);
-          lds_wait_group<0>(gbuf[1]);
-          SAS_TR_MMA(1, gbuf[1]);
-          static_assert(NG == 2, "two k-steps per 32-row tile");
-#undef SAS_TR_GROUP
-#undef SAS_TR_MMA
-        }
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const i16x4* g = gbuf[kq];
+            const i16x8 aop = {g[2 * e][0],     g[2 * e][1],     g[2 * e][2],     g[2 * e][3],
+                               g[2 * e + 1][0], g[2 * e + 1][1], g[2 * e + 1][2], g[2 * e + 1][3]};
+            acc[e] = Ops::mma(aop, pk[kq], acc[e]);
+          }
         // fp8 rows: stage (it + 2) % 3 last held tile it - 1, read before barrier A
         if constexpr (FP8) {
           if (more) fp8_store(fpt, (it + 2) % NSTAGE);
