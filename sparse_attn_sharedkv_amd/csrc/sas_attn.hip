@@ -284,7 +284,6 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   const int hlocal = hg * 32 + (lane & 31);  // head within the item's m-block
   const int hblocks = (a.num_heads + MB - 1) / MB;
   const int hl = lane >> 5;
-  const int my_rope_dma = (w < NROPE) ? 1 : 0;
   // Kᵀ operand: row lane%32, main chunk 16q + 2ks + hl, rope chunk 64 + 2q + hl
   const int r_qk = lane & 31;
   const int qk_base = main_row_base(r_qk) + (16 * q + hl) * 16;
@@ -467,10 +466,10 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         return (uint64_t)(uintptr_t)row_ptr(
             rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
       };
+      // (computed by every wave, without a branch; only waves w < NROPE use it)
       auto rope_ptr = [&](int tile) -> uint64_t {
-        return ROPE && w < NROPE
-                   ? (uint64_t)(uintptr_t)row_ptr(rowid[tile * TILE + 8 * w + (lane >> 3)])
-                   : (uint64_t)(uintptr_t)g_zero_row;
+        const int wr = ROPE && w < NROPE ? w : 0;
+        return (uint64_t)(uintptr_t)row_ptr(rowid[tile * TILE + 8 * wr + (lane >> 3)]);
       };
       // address of main row j from lane j (two v_readlane, no scalar arithmetic)
       auto lane_row = [&](uint64_t ptrs, int j) -> const char* {
@@ -526,18 +525,6 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       };
       Fp8Tile fpt;
 
-      // waits until at most the next tile's DMA instructions of this wave are in flight
-      auto wait_tile = [&](bool next_in_flight) {
-        if (!next_in_flight) {
-          wait_vmcnt<0>();
-        } else if (!ROPE || my_rope_dma == 0) {
-          wait_vmcnt<ROWS_PER_WAVE>();
-        } else if (my_rope_dma == 1) {
-          wait_vmcnt<ROWS_PER_WAVE + 1>();
-        } else {
-          wait_vmcnt<ROWS_PER_WAVE + 2>();
-        }
-      };
 
       if constexpr (FP8) {
         Fp8Tile f1;
@@ -566,43 +553,59 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       if (FP8 && ntile > 2) fp8_load(fpt, main_ptrs(2));
       __syncthreads();
 
+      // ---- Sᵀ partial of one tile over this wave's dims quarter (K operands 3 deep) ----
+      auto qk = [&](int stg) -> f32x16 {
+        const unsigned char* kb = kv_lds + stg * STAGE_BYTES;
+        auto kaddr = [&](int ks) -> const i16x8* {
+          return (const i16x8*)(ks < NKS_MAIN ? kb + qk_base + ks * 32 : kb + rope_off);
+        };
+        f32x16 r;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) r[j] = 0.0f;
+        constexpr int PF = 3;
+        i16x8 kbuf[PF];
+#pragma unroll
+        for (int i = 0; i < PF; ++i) kbuf[i] = *kaddr(i);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const i16x8 kop = kbuf[ks % PF];
+          if (ks + PF < NKS) kbuf[ks % PF] = *kaddr(ks + PF);
+          r = Ops::mma(kop, qf[ks], r);
+        }
+        return r;
+      };
+      // ---- reduce-scatter of the partials: quarter G's rows go to wave G ----
+      auto write_partials = [&](const f32x16& r) {
+#pragma unroll
+        for (int G = 0; G < NQ; ++G)
+          xpart[hg][G][q][lane] = (f32x4){r[4 * G], r[4 * G + 1], r[4 * G + 2], r[4 * G + 3]};
+      };
+
+      // Software pipeline over tiles. Iteration it runs Q·Kᵀ of tile it + 1 (its
+      // MFMAs execute under the softmax of tile it), the softmax and P·V of tile
+      // it, and publishes the partials of tile it + 1:
+      //   barrier A(it): partials of tile it visible; stage (it + 2) % 3 (tile
+      //                  it - 1's) free
+      //   barrier B(it): P of tile it visible
+      // Tile it + 2 must have landed before barrier A(it + 1), where tile it + 3
+      // is issued into the stage tile it's P·V has just released.
+      write_partials(qk(0));
+      __syncthreads();  // barrier A(0)
+      if (!FP8 && ntile > 2) issue(2, main_ptrs(2), rope_ptr(2));
+
       for (int it = 0; it < ntile; ++it) {
         const int stage = it % NSTAGE;
         const unsigned char* sb = kv_lds + stage * STAGE_BYTES;
-        // LDS words needed later in this tile, read now (latency hidden by Q·Kᵀ)
+        const bool has_next = it + 1 < ntile;
         const bool more = it + 2 < ntile;
+        // LDS words needed later in this iteration, read now
         const uint32_t vm_tile = tmask[it];
-        const int nx_tile = FP8 ? (it + 3 < ntile ? it + 3 : it) : (more ? it + 2 : it);
+        const int nx_tile = it + 3 < ntile ? it + 3 : it;
         uint64_t nx_main = main_ptrs(nx_tile);
         uint64_t nx_rope = FP8 ? 0ull : rope_ptr(nx_tile);
-        // ---- Sᵀ partial over this wave's dims quarter (K operands 3 deep) ----
-        f32x16 st;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) st[j] = 0.0f;
-        {
-          auto kaddr = [&](int ks) -> const i16x8* {
-            return (const i16x8*)(ks < NKS_MAIN ? sb + qk_base + ks * 32 : sb + rope_off);
-          };
-          constexpr int PF = 3;
-          i16x8 kbuf[PF];
-#pragma unroll
-          for (int i = 0; i < PF; ++i) kbuf[i] = *kaddr(i);
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            const i16x8 kop = kbuf[ks % PF];
-            if (ks + PF < NKS) kbuf[ks % PF] = *kaddr(ks + PF);
-            st = Ops::mma(kop, qf[ks], st);
-          }
-        }
-        // next DMA addresses: computed while the Q·Kᵀ MFMAs drain
-        pin_u64(nx_main);
-        if (!FP8) pin_u64(nx_rope);
-        // ---- reduce-scatter of the partials: quarter G's rows go to wave G ----
-#pragma unroll
-        for (int G = 0; G < NQ; ++G)
-          xpart[hg][G][q][lane] = (f32x4){st[4 * G], st[4 * G + 1], st[4 * G + 2], st[4 * G + 3]};
-        __syncthreads();  // barrier A
-        if (!FP8 && more) issue((it + 2) % NSTAGE, nx_main, nx_rope);
+        // ---- Q·Kᵀ of the next tile (results needed only after P·V; on the last
+        // tile it reads a stale stage and is discarded) ----
+        const f32x16 st_next = qk((it + 1) % NSTAGE);
 
         // fixed summation order over source quarters 0, 1, 2, 3
         const f32x4 sred = ((xpart[hg][q][0][lane] + xpart[hg][q][1][lane]) +
@@ -618,9 +621,10 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           mloc = fmaxf(mloc, sv[e]);
         }
         mloc = wave_max_pair(mloc);
-        if (hl == 0) mbuf[hg][q][lane & 31] = mloc;
+        // lanes l and l ^ 32 store the same value to the same word (no branch)
+        mbuf[hg][q][lane & 31] = mloc;
         const bool need_any = __any(mloc > m_run + RESCALE_TAU);
-        if (lane == 0) flags[w] = need_any ? 1 : 0;
+        flags[w] = need_any ? 1 : 0;
         float pv[4];
         auto make_p = [&]() {
           i16x4 pk4;
@@ -632,8 +636,14 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           *(i16x4*)(prow + pwr_off) = pk4;
         };
         make_p();
-        if (!FP8) wait_tile(more);  // this wave's share of tile it + 1 has landed
-        __syncthreads();  // barrier B
+        // next DMA addresses, computed before barrier B
+        pin_u64(nx_main);
+        if (!FP8) pin_u64(nx_rope);
+        __syncthreads();  // barrier B(it)
+        // fp8 rows: partials of tile it + 1 published here, so the Sᵀ registers are
+        // free during P·V (every wave has read tile it's partials before barrier
+        // B; on the last tile they are garbage and never read)
+        if (FP8) write_partials(st_next);
 
         // rescale votes, P operand of both k-steps and Vᵀ of the whole tile:
         // issued together, then one wait (none of the asm outputs is touched
@@ -693,10 +703,16 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
                                g[2 * e + 1][0], g[2 * e + 1][1], g[2 * e + 1][2], g[2 * e + 1][3]};
             acc[e] = Ops::mma(aop, pk[kq], acc[e]);
           }
-        // fp8 rows: stage (it + 2) % 3 last held tile it - 1, read before barrier A
+        // fp8 rows: stage (it + 2) % 3 last held tile it - 1, read before barrier A(it)
         if constexpr (FP8) {
           if (more) fp8_store(fpt, (it + 2) % NSTAGE);
           if (it + 3 < ntile) fp8_load(fpt, nx_main);
+        }
+        if (has_next) {
+          if (!FP8) write_partials(st_next);
+          if (!FP8) wait_vmcnt<0>();  // this wave's share of tile it + 2 has landed
+          __syncthreads();            // barrier A(it + 1)
+          if (!FP8 && it + 3 < ntile) issue((it + 3) % NSTAGE, nx_main, nx_rope);
         }
       }
       __syncthreads();  // rowid / tmask / ring are rewritten by the next chunk or item
