@@ -225,3 +225,46 @@ def test_unreferenced_nan_rows_do_not_leak():
     out, lse = _run(kb)
     assert torch.isfinite(out.float()).all()
     _check(out, lse, kb)
+
+
+def _fp8_pool(lens, seed, bs=64):
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    nblk = sum((x + bs - 1) // bs for x in lens) + 1
+    raw = torch.from_numpy(F.random_rows(nblk * bs, g)).reshape(nblk, bs, 1, 656)
+    return gen.paged_pool(seq_lens=lens, block_size=bs, block_num=nblk, head_dim=656,
+                          dtype=torch.uint8, rng=rng, values=lambda shape: raw.clone(),
+                          zero_unused=False)
+
+
+@requires_gpu
+@pytest.mark.parametrize("scenario", [1, 2, 3])
+def test_fp8_window_and_compressed_scenarios(scenario):
+    # SWA (scenario 1), SWA + dense compressed (2), SWA + top-k compressed (3) over fp8
+    # caches; two query rows per sequence (BSND, S = 2), sinks U(-1, 1)
+    _say(f"fp8 scenario {scenario}")
+    lens = [1500, 3000, 700]
+    g = torch.Generator().manual_seed(30 + scenario)
+    ori, ori_t = _fp8_pool(lens, 40 + scenario)
+    s_q, h, ratio = 2, 64, 4
+    kw = dict(q=(torch.randn(len(lens), s_q, h, 576, generator=g) * 0.5).to(torch.bfloat16),
+              ori_kv=ori, ori_block_table=ori_t, seqused_kv=torch.tensor(lens, dtype=torch.int32),
+              sinks=torch.rand(h, generator=g) * 2 - 1, softmax_scale=1 / 24.0,
+              ori_win_left=127, layout_q="BSND", head_dim_v=512, kv_cache_dtype="fp8_ds_mla")
+    if scenario >= 2:
+        cmp, cmp_t = _fp8_pool([x // ratio for x in lens], 50 + scenario)
+        kw.update(cmp_kv=cmp, cmp_block_table=cmp_t, cmp_ratio=ratio)
+    if scenario == 3:
+        k = 256
+        thr = [(x - s_q + s + 1) // ratio for x in lens for s in range(s_q)]
+        idx = gen.topk_indices(thresholds=thr, k=k, gen=g)
+        kw.update(cmp_sparse_indices=idx.reshape(len(lens), s_q, 1, k), topk_cmp=k)
+    from sparse_attn_sharedkv_amd import sparse_attn_sharedkv
+    out, lse = sparse_attn_sharedkv(**{k2: (v.cuda() if isinstance(v, torch.Tensor) else v)
+                                       for k2, v in kw.items()}, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    okw = {k2: v for k2, v in kw.items() if k2 != "topk_cmp"}
+    ref, ref_lse = sparse_attn_oracle(**okw)
+    ex, _ = sparse_attn_exact(**okw)
+    check_strict(out.cpu().reshape(ref.shape), ref, lse.cpu().reshape(ref_lse.shape), ref_lse)
+    check_vs_exact(out.cpu().reshape(ref.shape), ref, ex.reshape(ref.shape))
