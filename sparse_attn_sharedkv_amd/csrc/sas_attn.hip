@@ -11,22 +11,24 @@
 //   (shared KV, N2 = 1): a 32-row tile is loaded once into LDS and read by
 //   every wave, as K for Q·Kᵀ and (first head_dim_v columns) as V for P·V.
 //
-// Waves (NHG head groups of 32 heads; 2*NHG waves):
-//   wave w -> head group hg = w % NHG, half p = w / NHG.
-//   Q·Kᵀ: wave computes Sᵀ[32 rows x 32 heads] over dims half p of d_qk with
-//         v_mfma_f32_32x32x16 (A = K rows from LDS, B = Qᵀ held in VGPRs);
-//         the two halves of a head group are summed through LDS.
-//   softmax: each lane owns one head (lane % 32) and 16 of the 32 rows; the
-//         other 16 live in lane ^ 32. exp2 domain, lazy rescaling (the O
-//         rescale only runs when some head's max grows by > 2^8).
-//   P·V:  wave accumulates Oᵀ[dv half p x 32 heads] with the same MFMA
-//         (A = Vᵀ via ds_read_b64_tr_b16 from the row-major tile, B = Pᵀ
-//         straight from the Sᵀ accumulator layout, no data movement).
+// Waves (NHG head groups of 32 heads x 4 dims quarters = 4*NHG waves, two per
+// SIMD for the 64-head items of H > 32; details at attn_kernel):
+//   Q·Kᵀ: each wave computes a partial Sᵀ[32 rows x 32 heads] over its quarter
+//         of d_qk with v_mfma_f32_32x32x16 (A = K rows from LDS, B = Qᵀ held in
+//         VGPRs); the four partials of a head group are summed through LDS.
+//   softmax: exp2 domain on 4 rows x 1 head per lane; P shared through LDS;
+//         lazy rescaling (the O rescale only runs when some head's max grows
+//         by more than 2^8).
+//   P·V:  each wave accumulates Oᵀ[its dv quarter x 32 heads] (A = Vᵀ via
+//         ds_read_b64_tr_b16 from the row-major tile, B = Pᵀ from LDS).
+//   The tile loop is software-pipelined: Q·Kᵀ of the next tile is issued
+//   before the softmax of this one, so the two overlap.
 //
 // Gather: global_load_lds_dwordx4 (16 B per lane straight into LDS, no VGPR
 //   staging) into a 3-stage ring; rows of a tile are rotated by 16-byte
 //   chunks so both the Kᵀ reads (b128) and the transposed V reads (tr_b16)
-//   are bank-conflict free.
+//   are bank-conflict free. fp8 cache rows are loaded into VGPRs instead and
+//   dequantized into the same bf16 layout.
 //
 // Numerics follow golden.py:156-200: fp32 scores, P rounded to the input
 // dtype before P·V while the running sum uses fp32 P, out = acc / l rounded
@@ -232,9 +234,8 @@ __device__ inline i16x8 fp8x8_dequant_bf16(uint2 v, float s) {
 //         partial row sum (fp32 P) that is combined once per item.
 //   P·V:  wave q accumulates Oᵀ[dv quarter q (128) x 32 heads] over all rows.
 // Per tile: barrier A (partials written; the oldest stage is free for the
-// next DMA) and barrier B (P written; this tile's successor has landed). A
-// rescale (some head's max grew by more than 2^8) is decided workgroup-wide
-// after B and costs one more barrier.
+// next DMA) and barrier B (P written). A rescale (some head's max grew by more
+// than 2^8) is decided workgroup-wide after B and costs one more barrier.
 // fp8 rows (KVF = SAS_KV_FP8_DS_MLA): the main dims are loaded into VGPRs,
 // dequantized to bf16 and written to the same LDS layout, so every read of a
 // stage is the same as for a bf16 cache. Tile it + 2 is converted while tile
