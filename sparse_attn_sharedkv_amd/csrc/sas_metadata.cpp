@@ -12,6 +12,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <stdint.h>
+
 #include <algorithm>
 #include <string>
 #include <vector>
@@ -76,6 +78,23 @@ int greedy(const std::vector<Item>& items, int64_t c_item, int64_t budget, int64
   return cores;
 }
 
+// Largest per-core cost of a schedule given by its end cursors.
+int64_t makespan(const std::vector<Item>& items, int64_t c_item, const std::vector<Cursor>& ends) {
+  int64_t worst = 0;
+  Cursor s{0, 0};
+  for (const Cursor& e : ends) {
+    int64_t cost = 0;
+    for (size_t i = s.i; i < items.size() && (i < e.i || (i == e.i && e.j > 0)); ++i) {
+      const int64_t lo = i == s.i ? s.j : 0;
+      const int64_t hi = i == e.i ? e.j : items[i].nblk;
+      cost += c_item + (hi - lo);
+    }
+    worst = std::max(worst, cost);
+    s = e;
+  }
+  return worst;
+}
+
 }  // namespace
 
 extern "C" int sas_metadata_build(int32_t* meta, int batch, const int32_t* act_q,
@@ -129,6 +148,18 @@ extern "C" int sas_metadata_build(int32_t* meta, int batch, const int32_t* act_q
         lo = mid + 1;
     }
     greedy(items, c_item, lo, min_split_blocks, &ends);
+    // Splitting an item costs a merge kernel over its pieces (about
+    // SPLIT_PENALTY blocks of attention time): keep whole items when they fit
+    // the cores and the longest one is within that of the split makespan.
+    int64_t longest = 0;
+    for (const Item& it : items) longest = std::max(longest, c_item + it.nblk);
+    constexpr int64_t SPLIT_PENALTY = 3;
+    constexpr int64_t NO_SPLIT = INT64_MAX / 4;
+    if (longest <= makespan(items, c_item, ends) + SPLIT_PENALTY &&
+        greedy(items, c_item, longest, NO_SPLIT, nullptr) <= num_cores) {
+      ends.clear();
+      greedy(items, c_item, longest, NO_SPLIT, &ends);
+    }
     if ((int)ends.size() > num_cores) {
       sas::set_error("sas_metadata_build: schedule exceeds num_cores");
       return SAS_E_CAPACITY;
