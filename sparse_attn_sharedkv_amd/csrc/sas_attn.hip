@@ -775,21 +775,21 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
 // ---------------------------------------------------------------------------
 // Split-KV merge: lse = log(e^sink + Σ e^lse_i), out = Σ e^(lse_i - lse) o_i
 // ---------------------------------------------------------------------------
-// Grid: (merge task, group of MERGE_HPB heads). Each thread owns MERGE_PER
-// float4 of the group's rows and issues all of one piece's loads before using
-// them, so the pass is bandwidth- rather than latency-bound.
-constexpr int MERGE_MAX_PIECES = 32;  // pieces whose weights are staged in LDS
+// Grid: (merge task, group of MERGE_HPB heads). Thread t owns head t / 32 of
+// the group and float4 columns (t % 32) + 32 k: a half-wave reads 512
+// contiguous bytes per load. Each thread derives its head's weights itself
+// (the piece lse values are the same words for its 32 lanes), so there is no
+// LDS and no barrier, and the first two pieces' loads are in flight with the
+// lse, sink and token loads.
 constexpr int MERGE_HPB = 8;          // heads per workgroup
 constexpr int MERGE_THREADS = 256;
 
 template <int DV, typename T>
 __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs a) {
   constexpr int V4 = DV / 4;                              // float4 per head row
-  constexpr int PER = MERGE_HPB * V4 / MERGE_THREADS;     // float4 per thread
-  static_assert(MERGE_HPB * V4 % MERGE_THREADS == 0, "merge tiling");
-  static_assert(MERGE_MAX_PIECES * MERGE_HPB <= MERGE_THREADS, "one piece lse per thread");
-  __shared__ float lse_p[MERGE_MAX_PIECES][MERGE_HPB];  // piece lse, then piece weight
-  __shared__ float lse_s[MERGE_HPB];
+  constexpr int TPH = MERGE_THREADS / MERGE_HPB;          // threads per head (32)
+  constexpr int PER = V4 / TPH;                           // float4 per thread (4)
+  static_assert(V4 % TPH == 0 && TPH <= 64 && 64 % TPH == 0, "merge tiling");
   if (blockIdx.x >= (unsigned)a.num_fd) return;
   const int32_t* fd = a.metadata + SAS_FD_OFFSET + blockIdx.x * SAS_FD_METADATA_SIZE;
   if (fd[0] == 0) return;
@@ -801,84 +801,55 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
     return;
   const int g0 = (int)blockIdx.y * MERGE_HPB;  // first head of this group within the task
   if (g0 >= hn) return;
-  const int s = m / hblocks;
-  const int hbase = (m - s * hblocks) * mb + h0 + g0;  // query head of group row 0
-  const int hloc = h0 + g0;                            // m-block slot of group row 0
-  const int tok = a.q_prefix[b] + s;
-  if (tok < 0 || tok >= a.total_tokens) return;
+  const int tid = threadIdx.x;
+  const int hh = tid / TPH;
+  const int c0 = tid % TPH;
+  // rows past the task's last head (never stored) read that head's row instead
+  const int hr = g0 + hh < hn ? g0 + hh : hn - 1;
+  const int hloc = h0 + hr;                            // m-block slot of this thread's row
   const float* wo = a.workspace;
   const float* wl = a.workspace + (size_t)a.num_partial_slots * mb * DV;
-  const int tid = threadIdx.x;
-  const int nst = npc < MERGE_MAX_PIECES ? npc : MERGE_MAX_PIECES;  // pieces staged in LDS
-
-  int hh_of[PER], c4_of[PER];
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int e = tid + MERGE_THREADS * k;
-    hh_of[k] = e / V4;
-    c4_of[k] = e - hh_of[k] * V4;
-  }
-  // rows past the task's last head (never stored) read that head's row instead
-  int hr_of[PER];
-#pragma unroll
-  for (int k = 0; k < PER; ++k) hr_of[k] = g0 + hh_of[k] < hn ? hh_of[k] : hn - 1 - g0;
   auto piece = [&](int i, f32x4 (&v)[PER]) {
+    const float* src = wo + ((size_t)(slot0 + i) * mb + hloc) * DV + 4 * c0;
 #pragma unroll
     for (int k = 0; k < PER; ++k)  // all of one piece's loads in flight together
-      v[k] = *(const f32x4*)(wo + ((size_t)(slot0 + i) * mb + hloc + hr_of[k]) * DV + 4 * c4_of[k]);
+      v[k] = *(const f32x4*)(src + 4 * TPH * k);
   };
-  // the first two pieces are fetched before the weights are known
+  auto plse = [&](int i) -> float { return wl[(size_t)(slot0 + i) * mb + hloc]; };
   f32x4 v0[PER], v1[PER];
   piece(0, v0);
   if (npc > 1) piece(1, v1);
+  const int s = m / hblocks;
+  const int h = (m - s * hblocks) * mb + hloc;  // query head
+  const bool store = g0 + hh < hn && h < a.num_heads;
+  const float sink = a.sinks[h < a.num_heads ? h : a.num_heads - 1];
+  const int tok = a.q_prefix[b] + s;
+  const float l0 = plse(0);
+  const float l1 = npc > 1 ? plse(1) : -INFINITY;
 
-  // piece lse values: thread (i, hh) for i < nst, one load round
-  if (tid < nst * MERGE_HPB) {
-    const int i = tid / MERGE_HPB, hh = tid - i * MERGE_HPB;
-    lse_p[i][hh] = (g0 + hh < hn) ? wl[(size_t)(slot0 + i) * mb + hloc + hh] : -INFINITY;
+  // lse = log(e^sink + Σ_i e^lse_i); weights e^(lse_i - lse)
+  float mx = fmaxf(sink, l0);
+  if (npc > 1) mx = fmaxf(mx, l1);
+  for (int i = 2; i < npc; ++i) mx = fmaxf(mx, plse(i));
+  float l = -INFINITY;
+  if (mx != -INFINITY) {  // else no key and no sink: lse -inf, every weight 0
+    float tot = __expf(sink - mx) + __expf(l0 - mx);
+    if (npc > 1) tot += __expf(l1 - mx);
+    for (int i = 2; i < npc; ++i) tot += __expf(plse(i) - mx);
+    l = mx + __logf(tot);
   }
-  __syncthreads();
-  // per head: lse = log(e^sink + Σ_i e^lse_i); weights e^(lse_i - lse)
-  if (tid < MERGE_HPB) {
-    const int hh = tid;
-    const int h = hbase + hh;
-    float l = -INFINITY;
-    if (g0 + hh < hn && h < a.num_heads) {
-      const float sink = a.sinks[h];
-      float mx = sink;
-      for (int i = 0; i < nst; ++i) mx = fmaxf(mx, lse_p[i][hh]);
-      for (int i = nst; i < npc; ++i) mx = fmaxf(mx, wl[(size_t)(slot0 + i) * mb + hloc + hh]);
-      if (mx != -INFINITY) {  // else no key and no sink: lse -inf, every weight 0
-        float tot = __expf(sink - mx);
-        for (int i = 0; i < nst; ++i) tot += __expf(lse_p[i][hh] - mx);
-        for (int i = nst; i < npc; ++i) tot += __expf(wl[(size_t)(slot0 + i) * mb + hloc + hh] - mx);
-        l = mx + __logf(tot);
-      }
-    }
-    lse_s[hh] = l;
-    for (int i = 0; i < nst; ++i) {
-      const float li = lse_p[i][hh];
-      lse_p[i][hh] = (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
-    }
-  }
-  __syncthreads();
-
-  auto weight = [&](int i, int hh) -> float {
-    if (i < MERGE_MAX_PIECES) return lse_p[i][hh];
-    const float l = lse_s[hh];
-    const float li = wl[(size_t)(slot0 + i) * mb + hloc + hh];
+  auto weight = [&](float li) -> float {
     return (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
   };
   f32x4 o[PER];
+  const float w0 = weight(l0);
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const float w0 = weight(0, hh_of[k]);
+  for (int k = 0; k < PER; ++k)
     o[k] = (f32x4){w0 * v0[k][0], w0 * v0[k][1], w0 * v0[k][2], w0 * v0[k][3]};
-  }
   if (npc > 1) {
+    const float w1 = weight(l1);
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      const float w1 = weight(1, hh_of[k]);
       o[k][0] += w1 * v1[k][0]; o[k][1] += w1 * v1[k][1];
       o[k][2] += w1 * v1[k][2]; o[k][3] += w1 * v1[k][3];
     }
@@ -886,24 +857,22 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
   for (int i = 2; i < npc; ++i) {
     f32x4 v[PER];
     piece(i, v);
+    const float wi = weight(plse(i));
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      const float wi = weight(i, hh_of[k]);
       o[k][0] += wi * v[k][0]; o[k][1] += wi * v[k][1];
       o[k][2] += wi * v[k][2]; o[k][3] += wi * v[k][3];
     }
   }
+  if (!store || tok < 0 || tok >= a.total_tokens) return;
+  T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 4 * c0;
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
-    const int hh = hh_of[k];
-    const int h = hbase + hh;
-    if (g0 + hh >= hn || h >= a.num_heads) continue;
-    T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 4 * c4_of[k];
     const i16x4 pk = {MfmaOps<T>::from_f32(o[k][0]), MfmaOps<T>::from_f32(o[k][1]),
                       MfmaOps<T>::from_f32(o[k][2]), MfmaOps<T>::from_f32(o[k][3])};
-    *(i16x4*)orow = pk;
-    if (c4_of[k] == 0) a.lse[(size_t)tok * a.num_heads + h] = lse_s[hh];
+    *(i16x4*)(orow + 4 * TPH * k) = pk;
   }
+  if (c0 == 0) a.lse[(size_t)tok * a.num_heads + h] = l;
 }
 
 template <int DQK, int NHG, typename T, int KVF>
