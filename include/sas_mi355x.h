@@ -65,6 +65,8 @@ extern "C" {
 
 /* Scenario codes (api.py:196-202): 1 = SWA, 2 = CFA (dense compressed), 3 = SCFA (top-k). */
 
+#define SAS_SCHED_DEVICE (-1) /* SasAttnArgs.num_fd: schedule summary read on the device */
+
 /* Host-side scheduler (no GPU needed). Fills meta_out[SAS_META_SIZE].
  * act_q[b]: query rows of batch b; act_kv[b]: raw KV length of batch b.
  * m_base: heads per item (32 when num_heads <= 32, else 64).
@@ -77,6 +79,24 @@ int sas_metadata_build(int32_t* meta_out, int batch, const int32_t* act_q,
                        const int32_t* act_kv, int num_heads, int m_base, int ori_win_left,
                        int scenario, int cmp_ratio, int cmp_topk, int num_cores,
                        int s2_base, int min_split_blocks, int fd_head_chunk);
+
+/* On-device twin of sas_metadata_build (no reference counterpart: the reference
+ * schedules on the host, metadata.py:1018-1086). One workgroup on `stream` writes
+ * meta[SAS_META_SIZE] (device memory) from device-resident lengths: batch b has
+ * act_q[b] query rows (act_q: [batch] int32, device) or, when act_q is NULL,
+ * uniform_q rows; seqused_kv: [batch] int32 (device). Same algorithm and the same words as sas_metadata_build for the same
+ * lengths. Limits: batch <= SAS_DEV_SCHED_MAX_BATCH, items (query rows x head blocks)
+ * <= SAS_DEV_SCHED_MAX_ITEMS. Errors the host cannot see (a negative length, too many
+ * items, a schedule over capacity) leave the config row without SAS_META_MAGIC and
+ * its word 1 = -1 / -2 / -3; sas_attention_launch then writes NaN outputs.
+ * Asynchronous; returns SAS_E_INVALID for arguments checkable on the host. */
+#define SAS_DEV_SCHED_MAX_BATCH 4096
+#define SAS_DEV_SCHED_MAX_ITEMS 16384
+int sas_metadata_build_device(int32_t* meta, int batch, const int32_t* act_q,
+                              int uniform_q, const int32_t* seqused_kv, int num_heads,
+                              int m_base, int ori_win_left, int scenario, int cmp_ratio,
+                              int cmp_topk, int num_cores, int s2_base, int min_split_blocks,
+                              int fd_head_chunk, void* stream);
 
 /* Bytes of split-KV partial workspace for a schedule:
  * num_partial_slots * m_base * (head_dim_v + 1) * sizeof(float). */
@@ -122,7 +142,14 @@ typedef struct SasAttnArgs {
   int32_t cmp_block_num, cmp_block_size, cmp_table_len, topk;
   int32_t scenario, cmp_ratio, ori_win_left, dtype;
   float softmax_scale;
-  /* schedule summary (copies of the metadata config row, known to the host) */
+  /* schedule summary (copies of the metadata config row, known to the host). With
+   * num_fd == SAS_SCHED_DEVICE the kernels read the summary from the config row of
+   * `metadata` on the device instead (a schedule built by sas_metadata_build_device, or
+   * any schedule the host has not read back): num_fa is then the launch capacity (the
+   * schedule's core count must not exceed it; its FA rows fill [0, num_fa)),
+   * num_partial_slots the workspace capacity in slots, and s2_base is taken from the
+   * config row. A config row without SAS_META_MAGIC, or built for another head count,
+   * m_base or larger capacities, makes the launch write NaN to out and lse. */
   int32_t num_fa, num_fd, num_partial_slots, s2_base, m_base;
   /* kernels to enqueue: bit 0 attention, bit 1 split-KV merge; 0 means both.
    * A caller may enqueue the two phases as separate calls (attention first). */

@@ -29,6 +29,9 @@ DTYPE_FP16 = 1
 KV_NATIVE = 0
 KV_FP8_DS_MLA = 1
 FP8_ROW_BYTES = 656
+SCHED_DEVICE = -1             # SasAttnArgs.num_fd: schedule summary read on the device
+DEV_SCHED_MAX_BATCH = 4096
+DEV_SCHED_MAX_ITEMS = 16384
 
 
 class SasAttnArgs(ctypes.Structure):
@@ -76,8 +79,9 @@ class SasAttnArgs(ctypes.Structure):
     ]
 
 
-EXPORTS = ("sas_metadata_build", "sas_workspace_bytes", "sas_attention_launch",
-           "sas_kv_fp8_append", "sas_version", "sas_args_struct_size", "sas_last_error")
+EXPORTS = ("sas_metadata_build", "sas_metadata_build_device", "sas_workspace_bytes",
+           "sas_attention_launch", "sas_kv_fp8_append", "sas_version", "sas_args_struct_size",
+           "sas_last_error")
 
 _lock = threading.Lock()
 _lib = None
@@ -99,6 +103,10 @@ def load() -> ctypes.CDLL:
         i32p = ctypes.POINTER(ctypes.c_int32)
         lib.sas_metadata_build.restype = ctypes.c_int
         lib.sas_metadata_build.argtypes = [i32p, ctypes.c_int, i32p, i32p] + [ctypes.c_int] * 10
+        lib.sas_metadata_build_device.restype = ctypes.c_int
+        lib.sas_metadata_build_device.argtypes = ([ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                                   ctypes.c_int, ctypes.c_void_p] +
+                                                  [ctypes.c_int] * 10 + [ctypes.c_void_p])
         lib.sas_workspace_bytes.restype = ctypes.c_int64
         lib.sas_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.sas_attention_launch.restype = ctypes.c_int

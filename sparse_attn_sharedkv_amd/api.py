@@ -32,8 +32,8 @@ from typing import Optional, Tuple, Union
 import torch
 
 from . import _lib
-from .metadata import (DEFAULT_CORE_NUM, SAS_META_SIZE, build_metadata, config_row,  # noqa: F401
-                       m_base_for)
+from .metadata import (DEFAULT_CORE_NUM, DEFAULT_S2_BASE, SAS_META_SIZE,  # noqa: F401
+                       build_metadata, build_metadata_device, config_row, m_base_for)
 
 DEFAULT_BLOCK_I = 128  # kernel.py:65, kept for callers that import it
 SUPPORTED_HEAD_DIMS = (512, 576)
@@ -95,8 +95,16 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             layout_q: str = "TND", layout_kv: str = "PA_ND",
             core_num: int = DEFAULT_CORE_NUM, topk_cmp: Optional[int] = None,
             head_dim_v: Optional[int] = None,
-            kv_cache_dtype: Optional[str] = None) -> Prepared:
-    """Validate and stage one call (host work of api.py:186-384) without launching."""
+            kv_cache_dtype: Optional[str] = None,
+            schedule: Optional[str] = None) -> Prepared:
+    """Validate and stage one call (host work of api.py:186-384) without launching.
+
+    ``schedule``: ``"host"`` reads the lengths back and schedules on the CPU (the
+    reference's behaviour, api.py:335-360); ``"device"`` keeps them on the GPU and
+    runs the on-device scheduler (no host synchronisation); ``None`` means
+    ``"device"`` when ``metadata`` is a GPU tensor (it is then not read back) and
+    ``"host"`` otherwise.
+    """
     del seqused_q  # API-parity placeholder (api.py:186)
     assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
     assert cmp_mask_mode == 3 or cmp_kv is None, "only cmp_mask_mode=3 supported"
@@ -104,6 +112,10 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     assert layout_kv == "PA_ND", "only layout_kv=PA_ND supported"
     assert layout_q in ("TND", "BSND"), f"unsupported layout_q={layout_q!r}"
 
+    if schedule not in (None, "host", "device"):
+        raise ValueError(f"schedule must be 'host' or 'device', got {schedule!r}")
+    use_dev = schedule == "device" or (
+        schedule is None and metadata is not None and metadata.device.type == "cuda")
     dtype = q.dtype
     dcode = _dtype_code(dtype)
     if cmp_kv is None:
@@ -119,13 +131,18 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
         assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
         if q.dim() != 3:
             raise ValueError(f"TND q must be [T, N1, D], got {tuple(q.shape)}")
-        cu_host = [int(x) for x in cu_seqlens_q.to(torch.int32).cpu().tolist()]
-        nb = len(cu_host) - 1
-        act_q = [cu_host[i + 1] - cu_host[i] for i in range(nb)]
         t1, n1, d = q.shape
         total = t1
-        prefix = cu_host[:-1]
-        padded = (cu_host[-1] != t1) if cu_host else t1 > 0
+        if use_dev:  # lengths stay on the GPU; rows past cu_seqlens_q[-1] are zero-filled
+            nb = cu_seqlens_q.numel() - 1
+            act_q = prefix = None
+            padded = True
+        else:
+            cu_host = [int(x) for x in cu_seqlens_q.to(torch.int32).cpu().tolist()]
+            nb = len(cu_host) - 1
+            act_q = [cu_host[i + 1] - cu_host[i] for i in range(nb)]
+            prefix = cu_host[:-1]
+            padded = (cu_host[-1] != t1) if cu_host else t1 > 0
     else:
         if q.dim() != 4:
             raise ValueError(f"BSND q must be [B, S, N1, D], got {tuple(q.shape)}")
@@ -134,7 +151,10 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
         prefix = [i * s_max for i in range(nb)]
         act_q = [s_max] * nb
         padded = False
-        if cu_seqlens_q is not None:
+        if cu_seqlens_q is not None and use_dev:
+            act_q = None
+            padded = True
+        elif cu_seqlens_q is not None:
             cu_host = [int(x) for x in cu_seqlens_q.to(torch.int32).cpu().tolist()]
             act_q = [cu_host[i + 1] - cu_host[i] for i in range(nb)]
             padded = any(a != s_max for a in act_q)
@@ -194,7 +214,33 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
         raise RuntimeError("sparse_attn_sharedkv runs on a ROCm GPU; q is on " + str(dev))
 
     # ---- schedule (api.py:335-366) ----
-    if metadata is None:
+    i32 = torch.int32
+    seqused = seqused_kv.to(device=dev, dtype=i32).contiguous()
+    if use_dev:
+        # per-batch query rows and first flat token, computed on the GPU
+        if layout_q == "TND":
+            cu_d = cu_seqlens_q.to(device=dev, dtype=i32).reshape(-1)
+            act_q_d = (cu_d[1:] - cu_d[:-1]).contiguous()
+            q_prefix = cu_d[:-1].contiguous()
+        else:
+            q_prefix = torch.arange(nb, dtype=i32, device=dev) * (total // max(nb, 1))
+            if cu_seqlens_q is not None:
+                cu_d = cu_seqlens_q.to(device=dev, dtype=i32).reshape(-1)
+                act_q_d = (cu_d[1:] - cu_d[:-1]).contiguous()
+            else:
+                act_q_d = torch.full((nb,), total // max(nb, 1), dtype=i32, device=dev)
+        if metadata is None:
+            metadata_dev = build_metadata_device(
+                batch=nb, act_q=act_q_d, act_kv=seqused, num_heads=int(n1),
+                ori_win_left=int(ori_win_left), scenario=scenario, cmp_ratio=cmp_ratio_eff,
+                cmp_topk=int(k), core_num=int(core_num))
+        else:
+            metadata_dev = metadata.to(device=dev, dtype=i32).reshape(SAS_META_SIZE).contiguous()
+        # capacities; the kernels read the schedule's own summary on the GPU
+        cfg = dict(num_fa=int(core_num), num_fd=_lib.SCHED_DEVICE,
+                   num_partial_slots=2 * int(core_num), s2_base=DEFAULT_S2_BASE,
+                   m_base=m_base_for(n1))
+    elif metadata is None:
         kv_host = tuple(int(x) for x in seqused_kv.to(torch.int32).cpu().tolist())
         md = _cached_schedule(tuple(act_q), kv_host, int(n1), int(ori_win_left), scenario,
                               cmp_ratio_eff, int(k), int(core_num))
@@ -207,16 +253,15 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             "metadata was built for a different head count")
 
     # ---- device tensors ----
-    i32 = torch.int32
     q_flat = q.reshape(total, n1, d).contiguous()
     ori_kv_d = ori_kv.contiguous()
     ori_bt = ori_block_table.to(device=dev, dtype=i32).contiguous()
     cmp_kv_d = cmp_kv.contiguous() if cmp_kv is not None else None
     cmp_bt = cmp_block_table.to(device=dev, dtype=i32).contiguous() if cmp_kv is not None else None
     idx_d = idx_flat.to(device=dev, dtype=i32).contiguous() if idx_flat is not None else None
-    q_prefix = torch.tensor(prefix, dtype=i32).to(dev, non_blocking=True)
-    act_q_d = torch.tensor(act_q, dtype=i32).to(dev, non_blocking=True)
-    seqused = seqused_kv.to(device=dev, dtype=i32).contiguous()
+    if not use_dev:
+        q_prefix = torch.tensor(prefix, dtype=i32).to(dev, non_blocking=True)
+        act_q_d = torch.tensor(act_q, dtype=i32).to(dev, non_blocking=True)
     sinks_d = sinks.to(device=dev, dtype=torch.float32).contiguous()
     if sinks_d.numel() != n1:
         raise ValueError(f"sinks must have N1={n1} entries")
@@ -224,7 +269,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     out = alloc((total, n1, dv), dtype=dtype, device=dev)
     lse = alloc((total, n1), dtype=torch.float32, device=dev)
     ws = None
-    if cfg["num_fd"] > 0:
+    if cfg["num_fd"] > 0 or use_dev:
         nbytes = _lib.load().sas_workspace_bytes(cfg["num_partial_slots"], cfg["m_base"], dv)
         ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
 
@@ -311,6 +356,7 @@ def sparse_attn_sharedkv(
     topk_cmp: Optional[int] = None,
     head_dim_v: Optional[int] = None,
     kv_cache_dtype: Optional[str] = None,
+    schedule: Optional[str] = None,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Sparse shared-KV attention forward; returns ``attention_out`` in q's layout.
 
@@ -318,7 +364,9 @@ def sparse_attn_sharedkv(
     ``[T1, N1]`` (TND) or ``[B, S1, N1]`` (BSND), ``lse = max + ln(sum)`` over
     all attended keys with the sink folded in (api.py:176-184). ``metadata``
     is the output of ``sparse_attn_sharedkv_metadata``; when omitted it is
-    built here from the inputs (api.py:335-360).
+    built here from the inputs (api.py:335-360). ``schedule="device"`` builds it
+    on the GPU instead, so the call never waits for the device (see ``prepare``);
+    a ``metadata`` tensor on the GPU is used without being read back.
     """
     prep = prepare(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
                    ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
@@ -328,6 +376,6 @@ def sparse_attn_sharedkv(
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
                    core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
-                   kv_cache_dtype=kv_cache_dtype)
+                   kv_cache_dtype=kv_cache_dtype, schedule=schedule)
     launch(prep)
     return finalize(prep, return_softmax_lse)

@@ -199,6 +199,25 @@ __device__ inline void lds_wait_pv(uint64_t& votes, i16x8 (&p)[2], i16x4 (&g0)[8
 // unwritten pool row need not be. Large enough for every row format.
 __device__ __attribute__((aligned(256))) unsigned char g_zero_row[1152];
 
+// Device-built schedules (num_fd == SAS_SCHED_DEVICE): the summary is read from
+// the metadata config row; num_fa and num_partial_slots are the launch and
+// workspace capacities it must fit.
+__device__ inline bool dev_sched_ok(const SasAttnArgs& a, int mb) {
+  const int32_t* cfg = a.metadata + SAS_CFG_OFFSET;
+  return cfg[0] == SAS_META_MAGIC && cfg[5] == a.num_heads && cfg[6] == mb &&
+         cfg[2] >= 1 && cfg[2] <= a.num_fa && cfg[4] <= a.num_partial_slots &&
+         cfg[3] >= 0 && cfg[3] <= SAS_AIV_CORE_NUM && cfg[1] >= 32 && cfg[1] % 32 == 0;
+}
+// An unusable device-built schedule: every output becomes NaN (one workgroup).
+template <typename T>
+__device__ void nan_fill(const SasAttnArgs& a, int tid, int nthreads) {
+  const short qnan = __is_same(T, __bf16) ? (short)0x7FC0 : (short)0x7E00;
+  const size_t rows = (size_t)a.total_tokens * a.num_heads;
+  short* out = (short*)a.out;
+  for (size_t k = tid; k < rows * a.head_dim_v; k += nthreads) out[k] = qnan;
+  for (size_t k = tid; k < rows; k += nthreads) a.lse[k] = __builtin_nanf("");
+}
+
 // fp8 cache rows (SAS_KV_FP8_DS_MLA): eight e4m3 values (one 8-byte word) times
 // their block scale, each product rounded to bf16 (v_cvt_pk_f32_fp8 decodes OCP
 // e4m3 exactly; v_mul_f32 and v_cvt_pk_bf16_f32 round to nearest even).
@@ -300,8 +319,17 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   unsigned char* prow = &pbuf[hg][(lane & 31) * PSTRIDE];
   const int pwr_off = (16 * (q >> 1) + 8 * hl + 4 * (q & 1)) * 2;
 
+  int s2b = a.s2_base;
+  int nfa = a.num_fa;
+  if (a.num_fd == SAS_SCHED_DEVICE) {
+    if (!dev_sched_ok(a, MB)) {
+      if (blockIdx.x == 0) nan_fill<T>(a, tid, NT);
+      return;
+    }
+    s2b = a.metadata[SAS_CFG_OFFSET + 1];
+    nfa = a.metadata[SAS_CFG_OFFSET + 2];  // rows in use (the grid is sized for num_fa)
+  }
   // XCD-aware row mapping: consecutive FA rows (pieces of one item) share an XCD.
-  const int nfa = a.num_fa;
   const int per_xcd = (nfa + 7) >> 3;
   const int fa_row = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
   if (fa_row >= nfa || (int)(blockIdx.x >> 3) >= per_xcd) return;
@@ -311,7 +339,6 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   const int j_start = fa[3];
   const int b_end = fa[4], s_end = fa[5], j_end = fa[6];
   int slot = fa[7];
-  const int s2b = a.s2_base;
   const uint32_t kv_base = (uint32_t)(uintptr_t)kv_lds;
 
   const char* ori_kv = (const char*)a.ori_kv;
@@ -785,13 +812,12 @@ constexpr int MERGE_HPB = 8;          // heads per workgroup
 constexpr int MERGE_THREADS = 256;
 
 template <int DV, typename T>
-__global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs a) {
+__device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
   constexpr int V4 = DV / 4;                              // float4 per head row
   constexpr int TPH = MERGE_THREADS / MERGE_HPB;          // threads per head (32)
   constexpr int PER = V4 / TPH;                           // float4 per thread (4)
   static_assert(V4 % TPH == 0 && TPH <= 64 && 64 % TPH == 0, "merge tiling");
-  if (blockIdx.x >= (unsigned)a.num_fd) return;
-  const int32_t* fd = a.metadata + SAS_FD_OFFSET + blockIdx.x * SAS_FD_METADATA_SIZE;
+  const int32_t* fd = a.metadata + SAS_FD_OFFSET + task * SAS_FD_METADATA_SIZE;
   if (fd[0] == 0) return;
   const int mb = a.m_base;
   const int hblocks = (a.num_heads + mb - 1) / mb;
@@ -875,6 +901,18 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
   if (c0 == 0) a.lse[(size_t)tok * a.num_heads + h] = l;
 }
 
+// Tasks t = blockIdx.x, + gridDim.x, ... (one per workgroup column when the grid
+// matches the task count; device-built schedules launch for the capacity).
+template <int DV, typename T>
+__global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs a) {
+  int nfd = a.num_fd;
+  if (nfd == SAS_SCHED_DEVICE) {
+    if (!dev_sched_ok(a, a.m_base)) return;  // the attention kernel wrote NaN
+    nfd = a.metadata[SAS_CFG_OFFSET + 3];
+  }
+  for (int t = blockIdx.x; t < nfd; t += gridDim.x) merge_task<DV, T>(a, t);
+}
+
 template <int DQK, int NHG, typename T, int KVF>
 static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   const int phases = a.phases == 0 ? 3 : a.phases;
@@ -885,9 +923,11 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if ((phases & 2) && a.num_fd > 0) {
+  const bool dev = a.num_fd == SAS_SCHED_DEVICE;
+  if ((phases & 2) && (a.num_fd > 0 || dev)) {
     const int groups = (a.m_base + MERGE_HPB - 1) / MERGE_HPB;  // head groups per task (upper bound)
-    hipLaunchKernelGGL((merge_kernel<512, T>), dim3(a.num_fd, groups), dim3(MERGE_THREADS), 0, st,
+    const int tasks = dev ? (a.num_fa < 256 ? a.num_fa : 256) : a.num_fd;  // columns; tasks strided
+    hipLaunchKernelGGL((merge_kernel<512, T>), dim3(tasks, groups), dim3(MERGE_THREADS), 0, st,
                        a);
     return hipGetLastError();
   }
@@ -951,9 +991,10 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     set_error("sas_attention_launch: phases must be 0..3");
     return SAS_E_INVALID;
   }
-  if (a->num_fa < 1 || a->num_fa > SAS_AIC_CORE_NUM || a->num_fd < 0 ||
+  const bool dev_sched = a->num_fd == SAS_SCHED_DEVICE;
+  if (a->num_fa < 1 || a->num_fa > SAS_AIC_CORE_NUM || (a->num_fd < 0 && !dev_sched) ||
       a->num_fd > SAS_AIV_CORE_NUM || a->s2_base < 32 || (a->s2_base % 32) != 0 ||
-      (a->num_fd > 0 && (!a->workspace || a->num_partial_slots < 1))) {
+      ((a->num_fd > 0 || dev_sched) && (!a->workspace || a->num_partial_slots < 1))) {
     set_error("sas_attention_launch: inconsistent schedule");
     return SAS_E_INVALID;
   }

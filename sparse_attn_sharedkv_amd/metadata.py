@@ -107,6 +107,82 @@ def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: in
     return out
 
 
+def device_lengths(*, layout_q: str, layout_kv: str, device, cu_seqlens_q=None,
+                   cu_seqlens_ori_kv=None, seqused_q=None, seqused_kv=None, batch_size: int = 0,
+                   max_seqlen_q: int = 0, max_seqlen_kv: int = 0):
+    """``resolve_lengths`` on the GPU: ``(batch, act_q, uniform_q, act_kv)`` with int32
+    device tensors (``act_q`` is None when every batch has ``uniform_q`` rows). Only
+    tensor shapes are read on the host."""
+    i32 = torch.int32
+
+    def dev(t):
+        return torch.as_tensor(t).to(device=device, dtype=i32).reshape(-1)
+
+    def nonempty(t):
+        return t is not None and torch.as_tensor(t).numel() > 0
+
+    if nonempty(seqused_q):
+        batch = torch.as_tensor(seqused_q).numel()
+    elif layout_q == "TND" and nonempty(cu_seqlens_q):
+        batch = torch.as_tensor(cu_seqlens_q).numel() - 1
+    else:
+        batch = int(batch_size)
+    act_q, uniform_q = None, 0
+    if nonempty(seqused_q):
+        act_q = dev(seqused_q)[:batch].contiguous()
+    elif layout_q == "TND" and nonempty(cu_seqlens_q):
+        c = dev(cu_seqlens_q)
+        act_q = (c[1:batch + 1] - c[:batch]).contiguous()
+    else:
+        uniform_q = int(max_seqlen_q)
+    if nonempty(seqused_kv):
+        act_kv = dev(seqused_kv)[:batch].contiguous()
+    elif layout_kv == "TND" and nonempty(cu_seqlens_ori_kv):
+        c = dev(cu_seqlens_ori_kv)
+        act_kv = (c[1:batch + 1] - c[:batch]).contiguous()
+    else:
+        act_kv = torch.full((batch,), int(max_seqlen_kv), dtype=i32, device=device)
+    return batch, act_q, uniform_q, act_kv
+
+
+def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: torch.Tensor,
+                          num_heads: int, ori_win_left: int, scenario: int, cmp_ratio: int,
+                          cmp_topk: int, uniform_q: int = 0, core_num: int = DEFAULT_CORE_NUM,
+                          s2_base: int = DEFAULT_S2_BASE,
+                          min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
+                          fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK,
+                          stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """Run the on-device scheduler (``sas_metadata_build_device``) on the current stream.
+
+    ``act_q`` / ``act_kv``: int32 ``[batch]`` tensors on the GPU (``act_q`` None: every
+    batch has ``uniform_q`` query rows). Returns the int32 ``SAS_META_SIZE`` schedule on
+    the same GPU, word for word what ``build_metadata`` returns for the same lengths;
+    nothing is read back. Lengths the host cannot check (negative, too many items) leave
+    a schedule the attention launch turns into NaN outputs.
+    """
+    lib = _lib.load()
+    dev = act_kv.device
+    if dev.type != "cuda":
+        raise ValueError("build_metadata_device needs the lengths on a GPU")
+    if batch < 0 or batch > _lib.DEV_SCHED_MAX_BATCH:
+        raise ValueError(f"batch must be in [0, {_lib.DEV_SCHED_MAX_BATCH}] (got {batch})")
+    for t in (act_q, act_kv):
+        if t is not None and (t.dtype != torch.int32 or t.device != dev or t.numel() < batch
+                              or not t.is_contiguous()):
+            raise ValueError("act_q / act_kv must be contiguous int32 [batch] tensors on one GPU")
+    out = torch.empty(SAS_META_SIZE, dtype=torch.int32, device=dev)
+    st = stream if stream is not None else torch.cuda.current_stream(dev)
+    rc = lib.sas_metadata_build_device(
+        ctypes.c_void_p(out.data_ptr()), int(batch),
+        ctypes.c_void_p(act_q.data_ptr() if act_q is not None else 0), int(uniform_q),
+        ctypes.c_void_p(act_kv.data_ptr()), int(num_heads), m_base_for(int(num_heads)),
+        int(ori_win_left), int(scenario), int(cmp_ratio), int(cmp_topk), int(core_num),
+        int(s2_base), int(min_split_blocks), int(fd_head_chunk), ctypes.c_void_p(st.cuda_stream))
+    if rc < 0:
+        raise ValueError(_lib.last_error())
+    return out
+
+
 def config_row(metadata: torch.Tensor) -> dict:
     """Decode the schedule summary row (host copy; syncs if ``metadata`` is on a GPU)."""
     cfg = metadata.reshape(-1)[CFG_OFFSET:CFG_OFFSET + 8].to("cpu").tolist()
@@ -152,7 +228,10 @@ def sparse_attn_sharedkv_metadata(
     an empty raw window (golden.py:128-131 semantics, used for pure top-k
     decode). ``aic_core_num`` is the number of workgroups to balance over.
     ``aiv_core_num``, ``head_dim`` and ``ori_topk`` are accepted for signature
-    parity; merge tasks are bounded by ``AIV_CORE_NUM``.
+    parity; merge tasks are bounded by ``AIV_CORE_NUM``. With ``device`` a GPU the
+    schedule is built there by the on-device scheduler from the lengths moved to
+    (or already on) that GPU, without reading them back; the words are the ones
+    the host scheduler produces.
     """
     del cu_seqlens_cmp_kv, head_dim, ori_topk, aiv_core_num
     if num_heads_kv != 1:
@@ -169,6 +248,18 @@ def sparse_attn_sharedkv_metadata(
             raise ValueError("cmp_ratio must be >= 1 when a compressed cache is present")
     else:
         scenario = 1
+    core_num = min(int(aic_core_num), AIC_CORE_NUM)
+    if device is not None and torch.device(device).type == "cuda":
+        # scheduled on that GPU from device-resident lengths: nothing is read back
+        batch, act_q, uniform_q, act_kv = device_lengths(
+            layout_q=layout_q, layout_kv=layout_kv, device=device, cu_seqlens_q=cu_seqlens_q,
+            cu_seqlens_ori_kv=cu_seqlens_ori_kv, seqused_q=seqused_q, seqused_kv=seqused_kv,
+            batch_size=batch_size, max_seqlen_q=max_seqlen_q, max_seqlen_kv=max_seqlen_kv)
+        return build_metadata_device(batch=batch, act_q=act_q, uniform_q=uniform_q,
+                                     act_kv=act_kv, num_heads=num_heads_q,
+                                     ori_win_left=ori_win_left, scenario=scenario,
+                                     cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
+                                     core_num=core_num)
     act_q, act_kv = resolve_lengths(layout_q=layout_q, layout_kv=layout_kv,
                                     cu_seqlens_q=cu_seqlens_q,
                                     cu_seqlens_ori_kv=cu_seqlens_ori_kv, seqused_q=seqused_q,
@@ -177,5 +268,5 @@ def sparse_attn_sharedkv_metadata(
     md = build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads_q,
                         ori_win_left=ori_win_left, scenario=scenario,
                         cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
-                        core_num=min(int(aic_core_num), AIC_CORE_NUM))
+                        core_num=core_num)
     return md.to(device) if device is not None else md

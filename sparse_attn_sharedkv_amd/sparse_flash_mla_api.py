@@ -42,6 +42,7 @@ def sparse_flash_mla(
     topk_cmp: Optional[int] = None,
     head_dim_v: Optional[int] = 512,
     kv_cache_dtype: Optional[str] = None,
+    schedule: Optional[str] = None,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Sparse flash-MLA forward: ``attention_out`` (and lse) in q's layout."""
     prep = prepare(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
@@ -52,6 +53,6 @@ def sparse_flash_mla(
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
                    core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
-                   kv_cache_dtype=kv_cache_dtype)
+                   kv_cache_dtype=kv_cache_dtype, schedule=schedule)
     launch(prep)
     return finalize(prep, return_softmax_lse)

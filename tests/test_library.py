@@ -48,6 +48,9 @@ def test_header_constants_match_binding():
     assert int(consts["SAS_KV_NATIVE"]) == _lib.KV_NATIVE
     assert int(consts["SAS_KV_FP8_DS_MLA"]) == _lib.KV_FP8_DS_MLA
     assert int(consts["SAS_FP8_ROW_BYTES"]) == _lib.FP8_ROW_BYTES == 512 + 16 + 128
+    assert int(consts["SAS_SCHED_DEVICE"].strip("()")) == _lib.SCHED_DEVICE
+    assert int(consts["SAS_DEV_SCHED_MAX_BATCH"]) == _lib.DEV_SCHED_MAX_BATCH
+    assert int(consts["SAS_DEV_SCHED_MAX_ITEMS"]) == _lib.DEV_SCHED_MAX_ITEMS
 
 
 def test_fp8_writer_rejects_bad_arguments_without_a_gpu():
@@ -55,6 +58,29 @@ def test_fp8_writer_rejects_bad_arguments_without_a_gpu():
     assert lib.sas_kv_fp8_append(None, None, None, 4, 16, None) == -1
     assert lib.sas_kv_fp8_append(None, None, None, -1, 16, None) == -1
     assert lib.sas_kv_fp8_append(None, None, None, 0, 16, None) == 0   # nothing to do
+
+
+def test_device_scheduler_rejects_bad_arguments_without_a_gpu():
+    # host-checkable arguments are validated before any HIP call
+    lib = _lib.load()
+    good = dict(num_heads=64, m_base=64, win=127, scenario=1, ratio=1, topk=0, cores=256,
+                s2=64, split=2, chunk=32)
+
+    def call(meta=1, batch=1, act_q=None, uniform_q=1, act_kv=1, **kw):
+        a = dict(good, **kw)
+        return lib.sas_metadata_build_device(meta, batch, act_q, uniform_q, act_kv,
+                                             a["num_heads"], a["m_base"], a["win"], a["scenario"],
+                                             a["ratio"], a["topk"], a["cores"], a["s2"], a["split"],
+                                             a["chunk"], None)
+
+    assert call(meta=None) == -1
+    assert call(batch=_lib.DEV_SCHED_MAX_BATCH + 1) == -1
+    assert call(act_kv=None) == -1
+    assert call(uniform_q=-1) == -1
+    assert call(cores=_lib.AIC_CORE_NUM + 1) == -1
+    assert call(s2=48) == -1
+    assert call(scenario=2, ratio=0) == -1
+    assert "sas_metadata_build_device" in _lib.last_error()
 
 
 def test_workspace_bytes():
