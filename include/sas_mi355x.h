@@ -46,6 +46,13 @@ extern "C" {
  * (head_start / head_count are relative to the item's m-block, as fd_m_start / fd_m_num).
  * Config row (last 8 words): [SAS_META_MAGIC, s2_base, num_fa, num_fd,
  *                             num_partial_slots, num_heads, m_base, total_items]
+ * Schedule key (words [SAS_META_KEY_OFFSET, SAS_CFG_OFFSET), both schedulers write it;
+ * the kernels never read it): [SAS_KEY_MAGIC, items, batch, num_heads, m_base,
+ * ori_win_left, scenario, cmp_ratio, cmp_topk, num_cores, s2_base, min_split_blocks,
+ * fd_head_chunk, 0, 0, 0, query rows of each batch..., block count of each item...];
+ * word 0 is 0 when the inputs do not fit the key region. The device scheduler
+ * leaves a buffer that already holds the key of its inputs (and a valid config
+ * row) as it is: the schedule is a function of exactly these words.
  */
 #define SAS_AIC_CORE_NUM 512
 #define SAS_AIV_CORE_NUM 1024
@@ -55,6 +62,8 @@ extern "C" {
 #define SAS_META_SIZE 16384
 #define SAS_CFG_OFFSET (SAS_META_SIZE - 8)
 #define SAS_META_MAGIC 0x5A53A355
+#define SAS_META_KEY_OFFSET (SAS_FD_OFFSET + SAS_AIV_CORE_NUM * SAS_FD_METADATA_SIZE)
+#define SAS_KEY_MAGIC 0x5A53C0DE
 
 /* ---- error codes ---- */
 #define SAS_OK 0

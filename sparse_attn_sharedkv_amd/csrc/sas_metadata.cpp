@@ -6,7 +6,8 @@
 // tasks for items whose blocks land on more than one core. Differences, by
 // design: split-KV is enabled (the reference gates it off, metadata.py:323-325)
 // because decode has far fewer items than MI355X's 256 CUs; the budget is found
-// by bisection over a greedy fill instead of the reference's tolerance walk;
+// by a doubling search and bisection over a greedy fill instead of the
+// reference's tolerance walk;
 // blocks are s2_base positions of the item's concatenated [window ++ compressed]
 // list rather than separately aligned window / compressed 512-blocks.
 #include <stdio.h>
@@ -139,7 +140,13 @@ extern "C" int sas_metadata_build(int32_t* meta, int batch, const int32_t* act_q
   } else {
     int64_t total = 0;
     for (const Item& it : items) total += c_item + it.nblk;
-    int64_t lo = 1, hi = total;
+    // smallest budget whose fill fits num_cores: doubling search up from the
+    // average load (greedy(total) is one core, so it ends), then bisection
+    int64_t lo = 1, hi = std::max<int64_t>(1, (total + num_cores - 1) / num_cores);
+    while (hi < total && greedy(items, c_item, hi, min_split_blocks, nullptr) > num_cores) {
+      lo = hi + 1;
+      hi = std::min(total, 2 * hi);
+    }
     while (lo < hi) {
       const int64_t mid = lo + (hi - lo) / 2;
       if (greedy(items, c_item, mid, min_split_blocks, nullptr) <= num_cores)
@@ -229,6 +236,17 @@ extern "C" int sas_metadata_build(int32_t* meta, int batch, const int32_t* act_q
       row[6] = std::min(chunk, mb_heads - h0);
       ++nfd;
     }
+  }
+
+  // schedule key: every input the words above are a function of
+  int32_t* key = meta + SAS_META_KEY_OFFSET;
+  if (16 + (int64_t)batch + (int64_t)n <= SAS_CFG_OFFSET - SAS_META_KEY_OFFSET) {
+    const int32_t hdr[16] = {(int32_t)SAS_KEY_MAGIC, (int32_t)n, batch, num_heads, m_base,
+                             ori_win_left, scenario, cmp_ratio, cmp_topk, num_cores, s2_base,
+                             min_split_blocks, fd_head_chunk, 0, 0, 0};
+    for (int w = 0; w < 16; ++w) key[w] = hdr[w];
+    for (int b = 0; b < batch; ++b) key[16 + b] = act_q[b];
+    for (size_t i = 0; i < n; ++i) key[16 + batch + i] = (int32_t)items[i].nblk;
   }
 
   int32_t* cfg = meta + SAS_CFG_OFFSET;
