@@ -57,6 +57,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define SAS_LDS __attribute__((address_space(3)))
+#define SAS_GLOBAL __attribute__((address_space(1)))
 
 constexpr int TILE = 32;        // KV rows per pipeline stage
 constexpr int NSTAGE = 3;       // LDS ring depth
@@ -126,11 +127,15 @@ __device__ inline float wave_sum_pair(float v) {
 // unrelated LDS reads; completion is tracked by hand with s_waitcnt vmcnt.
 // An LDS DMA that reads M0 needs one wait state after the SALU write of M0
 // (the compiler's hazard pass cannot see inside the asm), hence the s_nop.
+// Rows are fetched with the streaming cache policy (sc0 nt): each row is read
+// once per workgroup (the second 64-head m-block of a token reads it on the
+// same XCD shortly after), and the non-temporal fills shortened the stalls of
+// the DMA issue on every tile (measured about 3.5 us of 66 at B = 64, H = 128).
 __device__ inline void dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
   asm volatile(
       "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, %1\n\t" ::"v"(voff),
+      "global_load_lds_dwordx4 %0, %1 sc0 nt\n\t" ::"v"(voff),
       "s"(sbase), "s"(lds_base)
       : "memory");
 }
@@ -138,7 +143,7 @@ __device__ inline void dma16_vaddr(const void* gptr, uint32_t lds_base) {
   asm volatile(
       "s_mov_b32 m0, %1\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off\n\t" ::"v"(gptr),
+      "global_load_lds_dwordx4 %0, off sc0 nt\n\t" ::"v"(gptr),
       "s"(lds_base)
       : "memory");
 }
@@ -171,6 +176,11 @@ template <int OFF>
 __device__ inline i16x8 ds_read_b128_asm(uint32_t addr) {
   i16x8 v;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+  return v;
+}
+__device__ inline uint32_t ds_read_b32_asm(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr) : "memory");
   return v;
 }
 __device__ inline uint64_t ds_read_b64_asm(uint32_t addr) {
@@ -529,16 +539,21 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         ropev rope;
       };
       constexpr int ROPE_LPR = 128 / RPL;  // lanes per row for the rope bytes
+      // (global, non-temporal loads: the rows stream through once, as the
+      // native rows' DMAs do)
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
       auto fp8_load = [&](Fp8Tile& f, uint64_t my_ptrs) {
         const char* rp = nullptr;
 #pragma unroll
         for (int j = 0; j < ROWS_PER_WAVE; ++j) {
           const char* p = lane_row(my_ptrs, j);
-          f.v[j] = *(const uint2*)(p + 8 * lane);
-          f.s[j] = *(const float*)(p + 512 + 4 * (lane >> 4));
+          const u32x2 t = __builtin_nontemporal_load((const SAS_GLOBAL u32x2*)(p + 8 * lane));
+          f.v[j] = make_uint2(t[0], t[1]);
+          f.s[j] = __builtin_nontemporal_load((const SAS_GLOBAL float*)(p + 512 + 4 * (lane >> 4)));
           rp = (lane / ROPE_LPR == j) ? p : rp;
         }
-        f.rope = *(const ropev*)(rp + ROPE_OFF + (lane % ROPE_LPR) * RPL);
+        f.rope = __builtin_nontemporal_load(
+            (const SAS_GLOBAL ropev*)(rp + ROPE_OFF + (lane % ROPE_LPR) * RPL));
       };
       auto fp8_store = [&](const Fp8Tile& f, int stage) {
         unsigned char* sb = kv_lds + stage * STAGE_BYTES;
@@ -626,18 +641,104 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         const unsigned char* sb = kv_lds + stage * STAGE_BYTES;
         const bool has_next = it + 1 < ntile;
         const bool more = it + 2 < ntile;
-        // LDS words needed later in this iteration, read now
-        const uint32_t vm_tile = tmask[it];
         const int nx_tile = it + 3 < ntile ? it + 3 : it;
-        uint64_t nx_main = main_ptrs(nx_tile);
-        uint64_t nx_rope = FP8 ? 0ull : rope_ptr(nx_tile);
-        // ---- Q·Kᵀ of the next tile (results needed only after P·V; on the last
-        // tile it reads a stale stage and is discarded) ----
-        const f32x16 st_next = qk((it + 1) % NSTAGE);
-
-        // fixed summation order over source quarters 0, 1, 2, 3
-        const f32x4 sred = ((xpart[hg][q][0][lane] + xpart[hg][q][1][lane]) +
-                            xpart[hg][q][2][lane]) + xpart[hg][q][3][lane];
+        // Vᵀ operands of this tile (the A operand of P·V)
+        const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
+        i16x4 gbuf[2][8];
+        auto read_vt = [&]() {
+#define SAS_TR_GROUP(GI, DST)                                                              \
+  {                                                                                        \
+    constexpr int q_ = (GI);                                                               \
+    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 0 * 64>(trb);                       \
+    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 0 * 64>(trb);              \
+    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 1 * 64>(trb);                       \
+    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 1 * 64>(trb);              \
+    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 2 * 64>(trb);                       \
+    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 2 * 64>(trb);              \
+    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 3 * 64>(trb);                       \
+    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 3 * 64>(trb);              \
+  }
+          SAS_TR_GROUP(0, gbuf[0]);
+          SAS_TR_GROUP(1, gbuf[1]);
+#undef SAS_TR_GROUP
+        };
+        uint32_t vm_tile;
+        uint64_t nx_main, nx_rope = 0;
+        f32x16 st_next;
+        f32x4 sred;
+        if constexpr (!FP8) {
+          // Every LDS read of the Q·Kᵀ / softmax phase is one ordered asm group,
+          // waited for by count: the tile mask and next-DMA row ids, Kᵀ of tile
+          // it + 1 and the partials of tile it; then the Vᵀ operands of tile it,
+          // so they stream in under the Q·Kᵀ MFMAs instead of between barrier B
+          // and P·V. (The fp8 form keeps the reads in source order: the extra
+          // live registers would spill there.)
+          vm_tile = ds_read_b32_asm((uint32_t)(uintptr_t)&tmask[it]);
+          uint32_t rid_main = ds_read_b32_asm((uint32_t)(uintptr_t)&rowid[
+              nx_tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
+          const int wr = ROPE && w < NROPE ? w : 0;
+          uint32_t rid_rope =
+              ds_read_b32_asm((uint32_t)(uintptr_t)&rowid[nx_tile * TILE + 8 * wr + (lane >> 3)]);
+          const unsigned char* kbn = kv_lds + ((it + 1) % NSTAGE) * STAGE_BYTES;
+          const uint32_t ka = (uint32_t)(uintptr_t)(kbn + qk_base);
+          i16x8 kq[NKS];
+          kq[0] = ds_read_b128_asm<0>(ka);
+          kq[1] = ds_read_b128_asm<32>(ka);
+          kq[2] = ds_read_b128_asm<64>(ka);
+          kq[3] = ds_read_b128_asm<96>(ka);
+          kq[4] = ds_read_b128_asm<128>(ka);
+          kq[5] = ds_read_b128_asm<160>(ka);
+          kq[6] = ds_read_b128_asm<192>(ka);
+          kq[7] = ds_read_b128_asm<224>(ka);
+          if constexpr (ROPE) kq[8] = ds_read_b128_asm<0>((uint32_t)(uintptr_t)(kbn + rope_off));
+          const uint32_t xa = (uint32_t)(uintptr_t)&xpart[hg][q][0][lane];
+          i16x8 xp[NQ];
+          xp[0] = ds_read_b128_asm<0>(xa);
+          xp[1] = ds_read_b128_asm<1024>(xa);
+          xp[2] = ds_read_b128_asm<2048>(xa);
+          xp[3] = ds_read_b128_asm<3072>(xa);
+          // mask, row ids and Kᵀ have landed (only the four partial reads may be
+          // pending; LDS reads of a wave complete in order). Each asm output
+          // register appears once: a duplicated operand makes the compiler copy
+          // the register before the wait, i.e. before the data has arrived.
+          if constexpr (ROPE)
+            asm volatile("s_waitcnt lgkmcnt(4)"
+                         : "+v"(vm_tile), "+v"(rid_main), "+v"(rid_rope), "+v"(kq[0]), "+v"(kq[1]),
+                           "+v"(kq[2]), "+v"(kq[3]), "+v"(kq[4]), "+v"(kq[5]), "+v"(kq[6]),
+                           "+v"(kq[7]), "+v"(kq[8])
+                         :
+                         : "memory");
+          else
+            asm volatile("s_waitcnt lgkmcnt(4)"
+                         : "+v"(vm_tile), "+v"(rid_main), "+v"(rid_rope), "+v"(kq[0]), "+v"(kq[1]),
+                           "+v"(kq[2]), "+v"(kq[3]), "+v"(kq[4]), "+v"(kq[5]), "+v"(kq[6]),
+                           "+v"(kq[7])
+                         :
+                         : "memory");
+          read_vt();
+          nx_main = (uint64_t)(uintptr_t)row_ptr(rid_main);
+          nx_rope = (uint64_t)(uintptr_t)row_ptr(rid_rope);
+          // ---- Q·Kᵀ of the next tile (results needed only after P·V; on the
+          // last tile it reads a stale stage and is discarded) ----
+#pragma unroll
+          for (int j = 0; j < 16; ++j) st_next[j] = 0.0f;
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) st_next = Ops::mma(kq[ks], qf[ks], st_next);
+          // the partials have landed (at most 15 of the 16 Vᵀ reads pending)
+          asm volatile("s_waitcnt lgkmcnt(15)"
+                       : "+v"(xp[0]), "+v"(xp[1]), "+v"(xp[2]), "+v"(xp[3])
+                       :
+                       : "memory");
+          // fixed summation order over source quarters 0, 1, 2, 3
+          sred = ((__builtin_bit_cast(f32x4, xp[0]) + __builtin_bit_cast(f32x4, xp[1])) +
+                  __builtin_bit_cast(f32x4, xp[2])) + __builtin_bit_cast(f32x4, xp[3]);
+        } else {
+          vm_tile = tmask[it];
+          nx_main = main_ptrs(nx_tile);
+          st_next = qk((it + 1) % NSTAGE);
+          sred = ((xpart[hg][q][0][lane] + xpart[hg][q][1][lane]) + xpart[hg][q][2][lane]) +
+                 xpart[hg][q][3][lane];
+        }
 
         // ---- online softmax (exp2 domain) on rows 8q + 4hl + jj ----
         const uint32_t vm = vm_tile >> (8 * q + 4 * hl);
@@ -673,31 +774,15 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         // B; on the last tile they are garbage and never read)
         if (FP8) write_partials(st_next);
 
-        // rescale votes, P operand of both k-steps and Vᵀ of the whole tile:
-        // issued together, then one wait (none of the asm outputs is touched
-        // before it)
-        const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
+        // rescale votes and the P operand of both k-steps (and, for fp8 rows,
+        // Vᵀ of the whole tile): issued together, then one wait (none of the
+        // asm outputs is touched before it)
         const uint32_t pka = (uint32_t)(uintptr_t)(prow + 16 * hl);
         uint64_t votes = ds_read_b64_asm((uint32_t)(uintptr_t)flags);
         i16x8 pk[2];
         pk[0] = ds_read_b128_asm<0>(pka);
         pk[1] = ds_read_b128_asm<32>(pka);
-        i16x4 gbuf[2][8];
-#define SAS_TR_GROUP(GI, DST)                                                              \
-  {                                                                                        \
-    constexpr int q_ = (GI);                                                               \
-    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 0 * 64>(trb);                       \
-    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 0 * 64>(trb);              \
-    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 1 * 64>(trb);                       \
-    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 1 * 64>(trb);              \
-    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 2 * 64>(trb);                       \
-    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 2 * 64>(trb);              \
-    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 3 * 64>(trb);                       \
-    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 3 * 64>(trb);              \
-  }
-        SAS_TR_GROUP(0, gbuf[0]);
-        SAS_TR_GROUP(1, gbuf[1]);
-#undef SAS_TR_GROUP
+        if constexpr (FP8) read_vt();
         lds_wait_pv(votes, pk, gbuf[0], gbuf[1]);
         if (__builtin_amdgcn_readfirstlane((uint32_t)(votes | (votes >> 32)))) {
           // rescale: every wave of the head group derives the same new max
@@ -722,6 +807,9 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         l_part += (pv[0] + pv[1]) + (pv[2] + pv[3]);
 
         // ---- Oᵀ += Vᵀ · Pᵀ over both 16-row k-steps ----
+        // (issue priority to this wave's MFMA chain while its SIMD partner runs
+        // VALU / LDS work)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kq = 0; kq < 2; ++kq)
 #pragma unroll
@@ -731,6 +819,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
                                g[2 * e + 1][0], g[2 * e + 1][1], g[2 * e + 1][2], g[2 * e + 1][3]};
             acc[e] = Ops::mma(aop, pk[kq], acc[e]);
           }
+        __builtin_amdgcn_s_setprio(0);
         // fp8 rows: stage (it + 2) % 3 last held tile it - 1, read before barrier A(it)
         if constexpr (FP8) {
           if (more) fp8_store(fpt, (it + 2) % NSTAGE);
