@@ -15,7 +15,17 @@ Shapes (BSND, block_size 64, q and KV ~ N(0, 1) * 0.5, softmax_scale = 1/sqrt(d_
                                      N(0, 1) * 0.5 quantized into 656-byte fp8 rows
                                      (``kv_fp8``)
 
-d_qk = 576 (512 latent + 64 rope), d_v = 512 throughout. Pure top-k attention
+Prefill (the reference's own 8K test shapes, test_sparse_attn_sharedkv.py:81-220:
+TND, one sequence of 8192 query rows over 8192 cached rows, H=64, d_qk = d_v =
+512, block_size 128, window 128, sinks U(-1,1)):
+
+* ``swa_prefill_t8192_h64``          sliding window only (scenario 1)
+* ``cfa_prefill_t8192_h64``          window + every compressed row below the
+                                     threshold, ratio 128 (scenario 2)
+* ``scfa_prefill_t8192_h64``         window + top-512 of the compressed rows, ratio 4
+                                     (scenario 3)
+
+Decode workloads: d_qk = 576 (512 latent + 64 rope), d_v = 512. Pure top-k attention
 is expressed through the reference API as a compressed cache equal to the raw
 pool with cmp_ratio 1 and an empty raw window (ori_win_left = -1). Block
 tables hand each sequence a random permutation slice of the pool; top-k rows
@@ -49,6 +59,15 @@ WORKLOADS: Dict[str, dict] = {
                                            ctx=(32768, 131072), K=2048, window=-1, cmp_ratio=1,
                                            mode="topk", sinks="none", kv="fp8_ds_mla",
                                            layout="TND"),
+    "swa_prefill_t8192_h64": dict(B=1, S=8192, H=64, D=512, DV=512, ctx=(8192, 8192), K=0,
+                                  window=127, cmp_ratio=None, mode="swa", sinks="uniform",
+                                  layout="TND", block=128, prefill=True),
+    "cfa_prefill_t8192_h64": dict(B=1, S=8192, H=64, D=512, DV=512, ctx=(8192, 8192), K=0,
+                                  window=127, cmp_ratio=128, mode="cfa", sinks="uniform",
+                                  layout="TND", block=128, prefill=True),
+    "scfa_prefill_t8192_h64": dict(B=1, S=8192, H=64, D=512, DV=512, ctx=(8192, 8192), K=512,
+                                   window=127, cmp_ratio=4, mode="swa+topk", sinks="uniform",
+                                   layout="TND", block=128, prefill=True),
 }
 
 FP8_POOL_CHUNK_ROWS = 1 << 20  # bf16 rows generated (then quantized) at a time
@@ -89,11 +108,30 @@ def _pool_fp8(lens, block_size, rng, gen, device):
     return pool, torch.as_tensor(table, dtype=torch.int32, device=device)
 
 
+def _topk_rows(thresholds: torch.Tensor, k: int, gen: torch.Generator) -> torch.Tensor:
+    """``[n, k]`` int32: row i holds a uniformly random k-subset of ``[0, thr_i)`` in
+    random order (``randperm(thr_i)[:k]`` in distribution), ``-1`` padded; one
+    batched sort instead of one permutation per row."""
+    n = thresholds.numel()
+    m = max(int(thresholds.max().item()) if n else 0, 1)
+    keys = torch.rand((n, m), generator=gen, device=thresholds.device)
+    col = torch.arange(m, device=thresholds.device)
+    keys = torch.where(col[None, :] < thresholds[:, None], keys, torch.full_like(keys, 2.0))
+    take = min(k, m)
+    idx = keys.argsort(dim=1)[:, :take].to(torch.int32)
+    valid = torch.arange(take, device=thresholds.device)[None, :] < thresholds[:, None].clamp(max=k)
+    out = torch.full((n, k), -1, dtype=torch.int32, device=thresholds.device)
+    out[:, :take] = torch.where(valid, idx, torch.full_like(idx, -1))
+    return out
+
+
 def build_workload(name: str, *, device="cuda", seed: int = 0, batch: Optional[int] = None,
-                   ctx_override: Optional[Sequence[int]] = None, block_size: int = 64,
+                   ctx_override: Optional[Sequence[int]] = None, block_size: Optional[int] = None,
                    dtype=torch.bfloat16) -> dict:
     """Keyword arguments of ``sparse_flash_mla`` for one input set (plus ``head_dim_v``)."""
     w = WORKLOADS[name]
+    if block_size is None:
+        block_size = w.get("block", 64)
     b = int(batch if batch is not None else w["B"])
     s_q, h, d, dv, k = w["S"], w["H"], w["D"], w["DV"], w["K"]
     dev = torch.device(device)
@@ -120,11 +158,15 @@ def build_workload(name: str, *, device="cuda", seed: int = 0, batch: Optional[i
     cmp_kv = cmp_bt = None
     if w["mode"] == "topk":
         cmp_kv, cmp_bt = ori_kv, ori_bt
-    elif w["mode"] == "swa+topk":
+    elif w["mode"] in ("swa+topk", "cfa"):
         cmp_kv, cmp_bt = _pool([x // w["cmp_ratio"] for x in lens], block_size, d, dtype, rng,
                                kvg, dev)
     idx = None
-    if k > 0:
+    if k > 0 and w.get("prefill"):
+        thr = torch.cat([((lens[bi] - s_q + torch.arange(s_q, device=dev) + 1) // w["cmp_ratio"])
+                         .clamp(min=0) for bi in range(b)])
+        idx = _topk_rows(thr, k, gen(3)).reshape(b, s_q, 1, k)
+    elif k > 0:
         ig = gen(3)
         idx = torch.full((b * s_q, k), -1, dtype=torch.int32, device=dev)
         for bi in range(b):
@@ -172,6 +214,8 @@ def workload_counts(args: dict) -> dict:
     valid = None
     if idx is not None:
         valid = (idx.reshape(b * s_q, -1) >= 0).sum(dim=1).cpu().tolist()
+    ratio = args.get("cmp_ratio")
+    dense_cmp = args.get("cmp_kv") is not None and idx is None  # scenario 2: rows [0, thr)
     rows = 0
     for bi in range(b):
         for s in range(s_q):
@@ -179,6 +223,8 @@ def workload_counts(args: dict) -> dict:
             rows += max(0, sg + 1 - max(sg - win, 0))
             if valid is not None:
                 rows += int(valid[bi * s_q + s])
+            elif dense_cmp:
+                rows += max(0, (sg + 1) // ratio)
     fp8 = args.get("kv_cache_dtype") == "fp8_ds_mla"
     return dict(tokens=b * s_q, rows=rows, heads=h, d_qk=d, d_v=dv,
                 k=idx.shape[-1] if idx is not None else 0, row_bytes=656 if fp8 else 2 * d)
