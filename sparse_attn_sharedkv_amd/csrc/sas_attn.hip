@@ -304,7 +304,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   __shared__ __attribute__((aligned(8))) unsigned char flags[8];  // per-wave rescale votes
   __shared__ uint32_t rowid[RCHUNK];
   __shared__ uint32_t tmask[RCHUNK / TILE];
-  __shared__ int first_neg;
+  __shared__ int first_neg[2];  // first -1 of the top-k scan, per item parity
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -355,7 +355,15 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
   const float sc = a.softmax_scale * LOG2E;
   if (tid < 8) flags[tid] = 0;  // bytes of absent waves stay 0
+  if (tid < 2) first_neg[tid] = INT32_MAX;
+  __syncthreads();
 
+  // Sinks of this lane's head in the (at most two) head blocks an item can
+  // have, loaded once: a load per item would also wait for the previous
+  // item's output stores (one in-order counter covers loads and stores).
+  const float sink_hb0 = hlocal < a.num_heads ? a.sinks[hlocal] : -INFINITY;
+  const float sink_hb1 = MB + hlocal < a.num_heads ? a.sinks[MB + hlocal] : -INFINITY;
+  int item_par = 0;  // which first_neg slot the next top-k scan uses
   bool first_item = true;
   for (;;) {
     // normalise the cursor: skip batches with no (more) query rows
@@ -390,7 +398,9 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
     // ---- online-softmax state: m shared by the head group, l partial per wave ----
     // (golden.py:156-160 seeds m = sink, l = 1: the 1 goes to one lane of quarter 0;
     // the row sums of lanes l and l ^ 32 (same head) are added at the end)
-    float m_run = partial ? -INFINITY : (head_ok ? a.sinks[head] * LOG2E : -INFINITY);
+    const int hb = m - s * hblocks;
+    const float sink_v = hb == 0 ? sink_hb0 : hb == 1 ? sink_hb1 : a.sinks[head_ok ? head : 0];
+    float m_run = partial ? -INFINITY : (head_ok ? sink_v * LOG2E : -INFINITY);
     float l_part = (partial || q != 0 || hl != 0) ? 0.0f : 1.0f;
     f32x16 acc[DVB];
 #pragma unroll
@@ -399,34 +409,18 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       for (int j = 0; j < 16; ++j) acc[d][j] = 0.0f;
 
     // ---- scenario 3: position of the first -1 among the scanned top-k slots ----
-    // (golden.py:48-53: the scan stops at the first -1). Loads are batched:
-    // every thread issues its SCAN_PER loads before testing any of them.
+    // (golden.py:48-53: the scan stops at the first -1). The first chunk's own
+    // top-k loads double as the scan of its range; the slots outside it are
+    // loaded in the same batch, and the block-table loads of the chunk are
+    // issued before the barrier that publishes the result (the -1 cut is
+    // applied when the row ids are packed). The two first_neg slots alternate
+    // between scans, so a slot is reset without a barrier of its own.
     const int32_t* idx_row =
         a.cmp_indices ? a.cmp_indices + (size_t)(tok_ok ? tok : 0) * a.topk : nullptr;
+    const bool scan3 = a.scenario == 3 && idx_row != nullptr && a.topk > 0;
+    const int jmax = (scan3 && p_hi > g.n_win) ? min(p_hi - g.n_win, g.n_cmp) : 0;
+    bool stop_pending = jmax > 0;
     int cmp_stop = g.n_cmp;
-    if (a.scenario == 3 && p_hi > g.n_win) {
-      if (tid == 0) first_neg = g.n_cmp;
-      __syncthreads();
-      const int jmax = min(p_hi - g.n_win, g.n_cmp);
-      constexpr int SCAN_PER = 8;
-      int mine = g.n_cmp;
-      for (int j0 = 0; j0 < jmax; j0 += NT * SCAN_PER) {
-        int v[SCAN_PER];
-#pragma unroll
-        for (int e = 0; e < SCAN_PER; ++e) {  // unconditional, clamped: all loads in flight at once
-          const int jj = j0 + e * NT + tid;
-          v[e] = idx_row[jj < jmax ? jj : jmax - 1];
-        }
-#pragma unroll
-        for (int e = 0; e < SCAN_PER; ++e) {
-          const int jj = j0 + e * NT + tid;
-          if (jj < jmax && v[e] == -1 && jj < mine) mine = jj;
-        }
-      }
-      if (mine < g.n_cmp) atomicMin(&first_neg, mine);
-      __syncthreads();
-      cmp_stop = first_neg;
-    }
 
     for (int c0 = p_lo; c0 < p_hi; c0 += RCHUNK) {
       const int clen = (p_hi - c0) < RCHUNK ? (p_hi - c0) : RCHUNK;
@@ -439,7 +433,6 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       int tab[PER];  // block-table word to read, or -1
       // Loads are unconditional with clamped, always in-bounds indices (so all
       // of a phase's loads are in flight together); results are masked after.
-      const bool scan3 = a.scenario == 3 && idx_row != nullptr && a.topk > 0;
 #pragma unroll
       for (int e = 0; e < PER; ++e) {
         const int r = e * NT + tid;
@@ -447,8 +440,37 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         const int jj = pos - g.n_win;
         int v = jj;
         if (scan3) v = idx_row[jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1)];
-        const bool live = r < clen && tok_ok && pos >= g.n_win && (a.scenario == 2 || jj < cmp_stop);
+        const bool live = r < clen && tok_ok && pos >= g.n_win;
         cid[e] = live ? v : -1;
+      }
+      if (stop_pending) {
+        // top-k slots [0, jmax) outside this chunk's own [own_lo, own_hi)
+        const int own_lo = max(c0 - g.n_win, 0);
+        const int own_hi = min(max(c0 + clen - g.n_win, own_lo), jmax);
+        const int n_extra = jmax - (own_hi - own_lo);
+        constexpr int SCAN_PER = 8;
+        int mine = g.n_cmp;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int jj = c0 + e * NT + tid - g.n_win;
+          if (jj >= 0 && jj < jmax && e * NT + tid < clen && cid[e] == -1 && jj < mine) mine = jj;
+        }
+        for (int x0 = 0; x0 < n_extra; x0 += NT * SCAN_PER) {
+          int v[SCAN_PER];
+#pragma unroll
+          for (int e = 0; e < SCAN_PER; ++e) {  // unconditional, clamped: all loads in flight at once
+            const int x = x0 + e * NT + tid;
+            const int xc = x < n_extra ? x : n_extra - 1;
+            v[e] = idx_row[xc < own_lo ? xc : xc + (own_hi - own_lo)];
+          }
+#pragma unroll
+          for (int e = 0; e < SCAN_PER; ++e) {
+            const int x = x0 + e * NT + tid;
+            const int jj = x < own_lo ? x : x + (own_hi - own_lo);
+            if (x < n_extra && v[e] == -1 && jj < mine) mine = jj;
+          }
+        }
+        if (mine < g.n_cmp) atomicMin(&first_neg[item_par], mine);
       }
 #pragma unroll
       for (int e = 0; e < PER; ++e) {
@@ -464,6 +486,13 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         const int t = (tbl != nullptr) ? tbl[(size_t)b * tlen + (bi < tlen ? bi : tlen - 1)] : -1;
         tab[e] = ok ? t : -1;
       }
+      if (stop_pending) {
+        __syncthreads();  // every thread's atomicMin is in
+        cmp_stop = min(first_neg[item_par], g.n_cmp);
+        if (tid == 0) first_neg[item_par ^ 1] = INT32_MAX;  // the next scan's slot
+        item_par ^= 1;
+        stop_pending = false;
+      }
 #pragma unroll
       for (int e = 0; e < PER; ++e) {
         const int r = e * NT + tid;
@@ -474,7 +503,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           if (pos < g.n_win) {
             if (phys < a.ori_block_num)
               id = (uint32_t)(phys * a.ori_block_size + (g.win_lo + pos) % a.ori_block_size);
-          } else if (phys < a.cmp_block_num) {
+          } else if (phys < a.cmp_block_num && (!scan3 || pos - g.n_win < cmp_stop)) {
             id = (uint32_t)(phys * a.cmp_block_size + cid[e] % a.cmp_block_size) | 0x80000000u;
           }
         }
