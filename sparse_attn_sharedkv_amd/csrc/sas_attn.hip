@@ -148,6 +148,13 @@ __device__ inline void dma16_vaddr(const void* gptr, uint32_t lds_base) {
       : "memory");
 }
 
+// A read-only kernel input at a wave-uniform address, as a scalar load (through
+// the constant address space: the compiler cannot prove on its own that the
+// kernel's stores leave these arrays alone, and would use a vector load).
+__device__ inline int32_t ld_uniform(const int32_t* p) {
+  return *(const __attribute__((address_space(4))) int32_t*)p;
+}
+
 // Materialise a value at this point of the program: the empty asm (ordered
 // with the barriers and the DMA asm) consumes it, so its computation cannot be
 // sunk past the next barrier towards its use.
@@ -358,16 +365,24 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   if (tid < 2) first_neg[tid] = INT32_MAX;
   __syncthreads();
 
-  // Sinks of this lane's head in the (at most two) head blocks an item can
-  // have, loaded once: a load per item would also wait for the previous
-  // item's output stores (one in-order counter covers loads and stores).
+  // Sinks of this lane's head in the (at most two: num_heads <= 128, 64-head
+  // items above 32 heads) head blocks of an item, loaded once: a load per
+  // item would also wait for the previous item's output stores (one in-order
+  // counter covers loads and stores). The wait the compiler can see keeps
+  // it from re-waiting at every use inside the item loop.
   const float sink_hb0 = hlocal < a.num_heads ? a.sinks[hlocal] : -INFINITY;
   const float sink_hb1 = MB + hlocal < a.num_heads ? a.sinks[MB + hlocal] : -INFINITY;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
   int item_par = 0;  // which first_neg slot the next top-k scan uses
   bool first_item = true;
   for (;;) {
+    // the cursor is uniform: keep it in SGPRs so the per-item length and
+    // prefix reads are scalar loads (a vector load here would wait for the
+    // previous item's output stores, which share its in-order counter)
+    b = __builtin_amdgcn_readfirstlane(b);
+    m = __builtin_amdgcn_readfirstlane(m);
     // normalise the cursor: skip batches with no (more) query rows
-    while (b < a.batch && b <= b_end && m >= a.act_q_lens[b] * hblocks) {
+    while (b < a.batch && b <= b_end && m >= ld_uniform(a.act_q_lens + b) * hblocks) {
       ++b;
       m = 0;
     }
@@ -378,9 +393,9 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
     const bool head_ok = head < a.num_heads;
     if (is_end && j_end == 0) break;
 
-    const int act_q = a.act_q_lens[b];
-    const int act_kv = a.seqused_kv[b];
-    const int tok = a.q_prefix[b] + s;
+    const int act_q = ld_uniform(a.act_q_lens + b);
+    const int act_kv = ld_uniform(a.seqused_kv + b);
+    const int tok = ld_uniform(a.q_prefix + b) + s;
     const ItemGeom g =
         item_geom(act_q, act_kv, s, a.ori_win_left, a.scenario, a.cmp_ratio, a.topk);
     const int L = g.n_win + g.n_cmp;
@@ -399,7 +414,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
     // (golden.py:156-160 seeds m = sink, l = 1: the 1 goes to one lane of quarter 0;
     // the row sums of lanes l and l ^ 32 (same head) are added at the end)
     const int hb = m - s * hblocks;
-    const float sink_v = hb == 0 ? sink_hb0 : hb == 1 ? sink_hb1 : a.sinks[head_ok ? head : 0];
+    const float sink_v = hb == 0 ? sink_hb0 : sink_hb1;
     float m_run = partial ? -INFINITY : (head_ok ? sink_v * LOG2E : -INFINITY);
     float l_part = (partial || q != 0 || hl != 0) ? 0.0f : 1.0f;
     f32x16 acc[DVB];
@@ -433,41 +448,87 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       int tab[PER];  // block-table word to read, or -1
       // Loads are unconditional with clamped, always in-bounds indices (so all
       // of a phase's loads are in flight together); results are masked after.
+      // (two branches: a load-free path must not inherit the top-k path's wait,
+      // which would also wait for the previous item's output stores)
+      // The -1 scan of the top-k slots [0, jmax) outside this chunk's own
+      // [own_lo, own_hi) (first chunk of a scanned item only): its first
+      // NT * SCAN_PER slots are loaded together with the chunk's own ids.
+      const int own_lo = max(c0 - g.n_win, 0);
+      const int own_hi = min(max(c0 + clen - g.n_win, own_lo), jmax);
+      const int n_extra = stop_pending ? jmax - (own_hi - own_lo) : 0;
+      constexpr int SCAN_PER = 4;
+      auto extra_slot = [&](int x) {  // x-th slot outside the own range
+        return x < own_lo ? x : x + (own_hi - own_lo);
+      };
+      int sv0[SCAN_PER];
+      if (scan3) {
+        // all loads issued, then one wait (as asm: the compiler gives such loads
+        // one destination register and a wait each)
+        int v[PER];
 #pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const int r = e * NT + tid;
-        const int pos = c0 + r;
-        const int jj = pos - g.n_win;
-        int v = jj;
-        if (scan3) v = idx_row[jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1)];
-        const bool live = r < clen && tok_ok && pos >= g.n_win;
-        cid[e] = live ? v : -1;
+        for (int e = 0; e < PER; ++e) {
+          const int jj = c0 + e * NT + tid - g.n_win;
+          const int32_t* src = idx_row + (jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1));
+          asm volatile("global_load_dword %0, %1, off" : "=v"(v[e]) : "v"(src) : "memory");
+        }
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) {
+          const int x = e * NT + tid;  // clamped into range; unused when n_extra == 0
+          const int xc = x < n_extra ? x : (n_extra > 0 ? n_extra - 1 : 0);
+          const int32_t* src = idx_row + (n_extra > 0 ? extra_slot(xc) : 0);
+          asm volatile("global_load_dword %0, %1, off" : "=v"(sv0[e]) : "v"(src) : "memory");
+        }
+        static_assert(PER == 2 || PER == 4, "resolution positions per thread");
+        static_assert(SCAN_PER == 4, "scan loads tied below");
+        if constexpr (PER == 2)
+          asm volatile("s_waitcnt vmcnt(0)"
+                       : "+v"(v[0]), "+v"(v[1]), "+v"(sv0[0]), "+v"(sv0[1]), "+v"(sv0[2]),
+                         "+v"(sv0[3])
+                       :
+                       : "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0)"
+                       : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(sv0[0]),
+                         "+v"(sv0[1]), "+v"(sv0[2]), "+v"(sv0[3])
+                       :
+                       : "memory");
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int r = e * NT + tid;
+          const int pos = c0 + r;
+          cid[e] = (r < clen && tok_ok && pos >= g.n_win) ? v[e] : -1;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int r = e * NT + tid;
+          const int pos = c0 + r;
+          cid[e] = (r < clen && tok_ok && pos >= g.n_win) ? pos - g.n_win : -1;
+        }
       }
       if (stop_pending) {
-        // top-k slots [0, jmax) outside this chunk's own [own_lo, own_hi)
-        const int own_lo = max(c0 - g.n_win, 0);
-        const int own_hi = min(max(c0 + clen - g.n_win, own_lo), jmax);
-        const int n_extra = jmax - (own_hi - own_lo);
-        constexpr int SCAN_PER = 8;
         int mine = g.n_cmp;
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
           const int jj = c0 + e * NT + tid - g.n_win;
           if (jj >= 0 && jj < jmax && e * NT + tid < clen && cid[e] == -1 && jj < mine) mine = jj;
         }
-        for (int x0 = 0; x0 < n_extra; x0 += NT * SCAN_PER) {
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) {
+          const int x = e * NT + tid;
+          if (x < n_extra && sv0[e] == -1 && extra_slot(x) < mine) mine = extra_slot(x);
+        }
+        for (int x0 = NT * SCAN_PER; x0 < n_extra; x0 += NT * SCAN_PER) {  // beyond the first round
           int v[SCAN_PER];
 #pragma unroll
           for (int e = 0; e < SCAN_PER; ++e) {  // unconditional, clamped: all loads in flight at once
             const int x = x0 + e * NT + tid;
-            const int xc = x < n_extra ? x : n_extra - 1;
-            v[e] = idx_row[xc < own_lo ? xc : xc + (own_hi - own_lo)];
+            v[e] = idx_row[extra_slot(x < n_extra ? x : n_extra - 1)];
           }
 #pragma unroll
           for (int e = 0; e < SCAN_PER; ++e) {
             const int x = x0 + e * NT + tid;
-            const int jj = x < own_lo ? x : x + (own_hi - own_lo);
-            if (x < n_extra && v[e] == -1 && jj < mine) mine = jj;
+            if (x < n_extra && v[e] == -1 && extra_slot(x) < mine) mine = extra_slot(x);
           }
         }
         if (mine < g.n_cmp) atomicMin(&first_neg[item_par], mine);
