@@ -243,3 +243,29 @@ def flops_and_bytes(counts: dict, kv_row_bytes: Optional[int] = None) -> tuple:
     flops = 2.0 * rows * h * (dq + dv)
     nbytes = rows * rb + t * h * dq * 2 + t * h * dv * 2 + t * h * 4 + t * k * 4 + rows * 4
     return flops, float(nbytes)
+
+
+def prefill_hbm_bytes(args: dict, counts: dict) -> float:
+    """Algorithmic HBM bytes of one prefill call: q, out and lse once, every
+    distinct cache row once (consecutive query rows re-read their neighbours'
+    window and compressed rows, which stay on chip), the top-k indices and one
+    block-table entry per distinct row."""
+    lens = [int(x) for x in args["seqused_kv"].cpu().tolist()]
+    b = len(lens)
+    t, h = counts["tokens"], counts["heads"]
+    dq, dv, k, rb = counts["d_qk"], counts["d_v"], counts["k"], counts["row_bytes"]
+    s_q = t // max(b, 1)
+    win = args["ori_win_left"]
+    ratio = args.get("cmp_ratio")
+    idx = args.get("cmp_sparse_indices")
+    rows = 0
+    for bi in range(b):
+        first = lens[bi] - s_q  # global position of the first query row
+        rows += lens[bi] - max(first - win, 0) if win >= 0 else 0
+        if args.get("cmp_kv") is not None and idx is None:
+            rows += max(0, lens[bi] // ratio)
+        elif idx is not None:
+            sel = idx.reshape(b, s_q, -1)[bi]
+            rows += int(torch.unique(sel[sel >= 0]).numel())
+    return float(rows * (rb + 4) + t * h * (dq * 2 + dv * 2 + 4) + t * k * 4)
+
