@@ -993,40 +993,77 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
                          mbuf[hg][2][lane & 31]) + mbuf[hg][3][lane & 31];
     __syncthreads();  // mbuf is reused by the next item
 
-    // ---- epilogue ----
-    if (tok_ok && head_ok) {
+    // ---- epilogue: the item's rows go out through LDS (the ring is free), so
+    // every store instruction writes whole rows (1 KB per wave) instead of
+    // 16- or 32-byte pieces of 32 rows ----
+    {
+      unsigned char* stg = kv_lds;
+      const int nh = min(MB, a.num_heads - hb * MB);  // heads of this item
+      // opaque copies of the thread indices: the addresses below are then
+      // computed here, not hoisted out of the item loop (where they would
+      // occupy registers across the tile loop)
+      int tid_e = tid, hl_e = hlocal, dv_e = q * (DV / NQ) + 4 * hl;
+      asm volatile("" : "+v"(tid_e), "+v"(hl_e), "+v"(dv_e));
       if (!partial) {
-        T* orow = (T*)a.out + ((size_t)tok * a.num_heads + head) * DV;
+        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes)
+        constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
+        static_assert(MB * SROW <= NSTAGE * STAGE_BYTES, "output staging");
         const float inv = 1.0f / l_run;
 #pragma unroll
         for (int d = 0; d < DVB; ++d)
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
-            const int dv = q * (DV / NQ) + 32 * d + 8 * g4 + 4 * hl;
+            const int dv = dv_e + 32 * d + 8 * g4;
             const i16x4 v = {Ops::from_f32(acc[d][4 * g4] * inv),
                              Ops::from_f32(acc[d][4 * g4 + 1] * inv),
                              Ops::from_f32(acc[d][4 * g4 + 2] * inv),
                              Ops::from_f32(acc[d][4 * g4 + 3] * inv)};
-            *(i16x4*)(orow + dv) = v;
+            *(i16x4*)(stg + hl_e * SROW + dv * 2) = v;
           }
-        if (q == 0 && hl == 0) a.lse[(size_t)tok * a.num_heads + head] = (m_run + __log2f(l_run)) * LN2;
+        __syncthreads();
+        if (tok_ok) {
+          char* obase = (char*)((T*)a.out + ((size_t)tok * a.num_heads + hb * MB) * DV);
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            *(i16x8*)(obase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
+          }
+          if (q == 0 && hl == 0 && head_ok)
+            a.lse[(size_t)tok * a.num_heads + hb * MB + hl_e] = (m_run + __log2f(l_run)) * LN2;
+        }
       } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
-        float* wo = a.workspace + ((size_t)slot * MB + hlocal) * DV;
+        // fp32 partials (acc / l), staged in two halves of the dv range
+        constexpr int HALF = DV / 2;
+        constexpr int SROW = HALF * 4 + 16;
+        constexpr int CPR = HALF * 4 / 16;
+        static_assert(MB * SROW <= NSTAGE * STAGE_BYTES, "partial staging");
         const bool empty = !(l_run > 0.0f);
         const float inv = empty ? 0.0f : 1.0f / l_run;
+        char* wbase = (char*)(a.workspace + (size_t)slot * MB * DV);
 #pragma unroll
-        for (int d = 0; d < DVB; ++d)
+        for (int half = 0; half < 2; ++half) {
+          if (half) __syncthreads();  // the first half has been read out
+          if ((q >> 1) == half) {  // waves whose dv quarter lies in this half
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const int dv = q * (DV / NQ) + 32 * d + 8 * g4 + 4 * hl;
-            f32x4 v;
+            for (int d = 0; d < DVB; ++d)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[d][4 * g4 + e] * inv;
-            *(f32x4*)(wo + dv) = v;
+              for (int g4 = 0; g4 < 4; ++g4) {
+                const int dv = dv_e - half * HALF + 32 * d + 8 * g4;  // within the half
+                f32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[d][4 * g4 + e] * inv;
+                *(f32x4*)(stg + hl_e * SROW + dv * 4) = v;
+              }
           }
-        if (q == 0 && hl == 0) {
+          __syncthreads();
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            *(f32x4*)(wbase + ((size_t)h * DV + half * HALF) * 4 + c16 * 16) =
+                *(const f32x4*)(stg + h * SROW + c16 * 16);
+          }
+        }
+        if (q == 0 && hl == 0 && head_ok) {
           float* wl = a.workspace + (size_t)a.num_partial_slots * MB * DV;
-          wl[(size_t)slot * MB + hlocal] =
+          wl[(size_t)slot * MB + hl_e] =
               empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
         }
       }
