@@ -1186,7 +1186,18 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
     if (!dev_sched_ok(a, a.m_base)) return;  // the attention kernel wrote NaN
     nfd = a.metadata[SAS_CFG_OFFSET + 3];
   }
-  for (int t = blockIdx.x; t < nfd; t += gridDim.x) merge_task<DV, T>(a, t);
+  // Tasks in eight slices: column bx runs on XCD bx % 8 (workgroups go round-
+  // robin over the 8 XCDs and the grid width is a multiple of 8) and takes the
+  // tasks of slice bx % 8. The attention kernel keeps consecutive FA rows on
+  // one XCD, so an evenly spread schedule leaves each slice's partials in that
+  // XCD's L2.
+  const int per = (nfd + 7) >> 3;
+  const int cols = (int)gridDim.x >> 3;
+  const int x = (int)blockIdx.x & 7;
+  for (int j = (int)blockIdx.x >> 3; j < per; j += cols) {
+    const int t = x * per + j;
+    if (t < nfd) merge_task<DV, T>(a, t);
+  }
 }
 
 template <int DQK, int NHG, typename T, int KVF>
@@ -1203,8 +1214,8 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   if ((phases & 2) && (a.num_fd > 0 || dev)) {
     const int groups = (a.m_base + MERGE_HPB - 1) / MERGE_HPB;  // head groups per task (upper bound)
     const int tasks = dev ? (a.num_fa < 256 ? a.num_fa : 256) : a.num_fd;  // columns; tasks strided
-    hipLaunchKernelGGL((merge_kernel<512, T>), dim3(tasks, groups), dim3(MERGE_THREADS), 0, st,
-                       a);
+    const int cols = (tasks + 7) / 8 * 8;  // a multiple of the 8 XCDs
+    hipLaunchKernelGGL((merge_kernel<512, T>), dim3(cols, groups), dim3(MERGE_THREADS), 0, st, a);
     return hipGetLastError();
   }
   return hipSuccess;
