@@ -3,7 +3,8 @@
 Cases follow the reference's suites: decode at kv = 8193 for SWA / CFA / SCFA
 in bf16 and fp16 (test_sparse_attn_sharedkv.py:81-235, :586-605), the shrunk
 prefill cases including the ragged two-sequence ones
-(test_sparse_attn_sharedkv_fast.py:147-179), the return-type contract
+(test_sparse_attn_sharedkv_fast.py:147-179), the full 8K prefill cases on
+sampled query rows, the return-type contract
 (:608-715) and the metadata-then-kernel flow (:484-583). Beyond them: the
 benchmark shapes (H = 16 / 64 / 128, d_qk = 576 with d_v = 512, pure top-k,
 MTP), split-KV invariance, index edge cases, and the full-size DeepSeek-V3.2
@@ -111,6 +112,28 @@ def test_reference_fast_prefill(name):
     kw = gen.build_case(gen.FAST_CASES[name], torch.bfloat16)
     out, lse = _run(kw)
     _check_reference_regime(out, lse, kw, torch.bfloat16)
+
+
+@requires_gpu
+@pytest.mark.parametrize("name", ["swa_prefill", "cfa_prefill", "scfa_prefill"])
+def test_reference_prefill_full_size_sampled_tokens(name):
+    # the reference's own 8K prefill cases (test_sparse_attn_sharedkv.py:105-220)
+    # at full size; the oracle checks query rows at the start, around the window
+    # and compressed-threshold edges, in the middle and at the end
+    _say(f"full-size reference prefill {name} (sampled)")
+    kw = gen.build_case(gen.REFERENCE_CASES[name], torch.bfloat16)
+    out, lse = _run(kw)
+    total = kw["q"].shape[0]
+    toks = sorted({0, 1, 3, 126, 127, 128, 129, 511, 512, 2047, 2048, 2049, 4095, 6143,
+                   total - 2, total - 1})
+    okw = {k: v for k, v in _cpu(kw).items() if k not in ("topk_cmp",)}
+    ref, ref_lse = sparse_attn_oracle(**okw, tokens=toks)
+    ex, _ = sparse_attn_exact(**okw, tokens=toks)
+    o, l = out.cpu()[toks], lse.cpu()[toks]
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    check_result(o, ref[toks])
+    check_lse(l, ref_lse[toks], torch.bfloat16)
+    check_vs_exact(o, ref[toks], ex[toks])
 
 
 @requires_gpu
