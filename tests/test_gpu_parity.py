@@ -191,6 +191,22 @@ def test_benchmark_shapes_reduced(name, batch):
 
 
 @requires_gpu
+@pytest.mark.parametrize("heads,d", [(16, 576), (48, 576), (96, 576), (48, 512), (112, 512)])
+@pytest.mark.parametrize("cores", [None, 5])
+def test_partial_head_blocks(heads, d, cores, monkeypatch):
+    # head counts that leave the last 32/64-head block partly empty (lanes without
+    # a head), with and without split items (5 cores: every item in pieces)
+    from sparse_attn_sharedkv_amd import workloads as wl
+    _say(f"partial head blocks H={heads} d={d} cores={cores}")
+    w = dict(wl.WORKLOADS["swa_topk_decode_b32_h64_k512"], H=heads, D=d, ctx=(3000, 9000))
+    monkeypatch.setitem(wl.WORKLOADS, "_partial_heads", w)
+    kw = gen.build_workload("_partial_heads", device="cuda", seed=heads + d, batch=4)
+    extra = {"core_num": cores} if cores else {}
+    out, lse = _run(kw, fn=sparse_flash_mla, **extra)
+    _check_benchmark_regime(out, lse, kw)
+
+
+@requires_gpu
 def test_swa_topk_short_context_pads_minus_one():
     # one sequence with thr < K so the index rows carry -1 padding
     _say("swa+topk short context")
