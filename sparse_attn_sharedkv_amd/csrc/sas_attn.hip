@@ -1118,52 +1118,89 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
       v[k] = *(const f32x4*)(src + 4 * TPH * k);
   };
   auto plse = [&](int i) -> float { return wl[(size_t)(slot0 + i) * mb + hloc]; };
-  f32x4 v0[PER], v1[PER];
-  piece(0, v0);
-  if (npc > 1) piece(1, v1);
   const int s = m / hblocks;
   const int h = (m - s * hblocks) * mb + hloc;  // query head
   const bool store = g0 + hh < hn && h < a.num_heads;
   const float sink = a.sinks[h < a.num_heads ? h : a.num_heads - 1];
   const int tok = a.q_prefix[b] + s;
-  const float l0 = plse(0);
-  const float l1 = npc > 1 ? plse(1) : -INFINITY;
-
-  // lse = log(e^sink + Σ_i e^lse_i); weights e^(lse_i - lse)
-  float mx = fmaxf(sink, l0);
-  if (npc > 1) mx = fmaxf(mx, l1);
-  for (int i = 2; i < npc; ++i) mx = fmaxf(mx, plse(i));
+  // lse = log(e^sink + Σ_i e^lse_i); weights e^(lse_i - lse); the sums keep the
+  // piece order 0, 1, 2, ...
+  f32x4 o[PER];
   float l = -INFINITY;
-  if (mx != -INFINITY) {  // else no key and no sink: lse -inf, every weight 0
-    float tot = __expf(sink - mx) + __expf(l0 - mx);
-    if (npc > 1) tot += __expf(l1 - mx);
-    for (int i = 2; i < npc; ++i) tot += __expf(plse(i) - mx);
-    l = mx + __logf(tot);
-  }
   auto weight = [&](float li) -> float {
     return (l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l);
   };
-  f32x4 o[PER];
-  const float w0 = weight(l0);
-#pragma unroll
-  for (int k = 0; k < PER; ++k)
-    o[k] = (f32x4){w0 * v0[k][0], w0 * v0[k][1], w0 * v0[k][2], w0 * v0[k][3]};
-  if (npc > 1) {
-    const float w1 = weight(l1);
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      o[k][0] += w1 * v1[k][0]; o[k][1] += w1 * v1[k][1];
-      o[k][2] += w1 * v1[k][2]; o[k][3] += w1 * v1[k][3];
+  if (npc <= 2) {
+    // one or two pieces: both fetched before the weights are known
+    f32x4 v0[PER], v1[PER];
+    piece(0, v0);
+    if (npc > 1) piece(1, v1);
+    const float l0 = plse(0);
+    const float l1 = npc > 1 ? plse(1) : -INFINITY;
+    float mx = fmaxf(sink, l0);
+    if (npc > 1) mx = fmaxf(mx, l1);
+    if (mx != -INFINITY) {  // else no key and no sink: lse -inf, every weight 0
+      float tot = __expf(sink - mx) + __expf(l0 - mx);
+      if (npc > 1) tot += __expf(l1 - mx);
+      l = mx + __logf(tot);
     }
-  }
-  for (int i = 2; i < npc; ++i) {
-    f32x4 v[PER];
-    piece(i, v);
-    const float wi = weight(plse(i));
+    const float w0 = weight(l0);
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      o[k][0] += wi * v[k][0]; o[k][1] += wi * v[k][1];
-      o[k][2] += wi * v[k][2]; o[k][3] += wi * v[k][3];
+    for (int k = 0; k < PER; ++k)
+      o[k] = (f32x4){w0 * v0[k][0], w0 * v0[k][1], w0 * v0[k][2], w0 * v0[k][3]};
+    if (npc > 1) {
+      const float w1 = weight(l1);
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        o[k][0] += w1 * v1[k][0]; o[k][1] += w1 * v1[k][1];
+        o[k][2] += w1 * v1[k][2]; o[k][3] += w1 * v1[k][3];
+      }
+    }
+  } else {
+    // more pieces: their data in batches of PB with all loads of a batch in
+    // flight together, the first MAXL lse values in one batch (a loop of one
+    // piece per round trip costs a memory latency per piece)
+    constexpr int PB = 4;
+    constexpr int MAXL = 16;
+    f32x4 vb[PB][PER];
+#pragma unroll
+    for (int i = 0; i < PB; ++i) piece(i < npc ? i : npc - 1, vb[i]);
+    float lv[MAXL];
+#pragma unroll
+    for (int i = 0; i < MAXL; ++i) lv[i] = plse(i < npc ? i : npc - 1);
+    auto lse_of = [&](int i) -> float { return i < MAXL ? lv[i] : plse(i); };
+    float mx = fmaxf(sink, lv[0]);
+#pragma unroll
+    for (int i = 1; i < MAXL; ++i)
+      if (i < npc) mx = fmaxf(mx, lv[i]);
+    for (int i = MAXL; i < npc; ++i) mx = fmaxf(mx, plse(i));
+    if (mx != -INFINITY) {
+      float tot = __expf(sink - mx) + __expf(lv[0] - mx);
+#pragma unroll
+      for (int i = 1; i < MAXL; ++i)
+        if (i < npc) tot += __expf(lv[i] - mx);
+      for (int i = MAXL; i < npc; ++i) tot += __expf(plse(i) - mx);
+      l = mx + __logf(tot);
+    }
+    for (int i0 = 0; i0 < npc; i0 += PB) {
+      if (i0 > 0) {
+#pragma unroll
+        for (int i = 0; i < PB; ++i) piece(i0 + i < npc ? i0 + i : npc - 1, vb[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        if (i0 + i >= npc) break;
+        const float wi = weight(lse_of(i0 + i));
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+          if (i0 + i == 0) {
+            o[k] = (f32x4){wi * vb[i][k][0], wi * vb[i][k][1], wi * vb[i][k][2], wi * vb[i][k][3]};
+          } else {
+            o[k][0] += wi * vb[i][k][0]; o[k][1] += wi * vb[i][k][1];
+            o[k][2] += wi * vb[i][k][2]; o[k][3] += wi * vb[i][k][3];
+          }
+        }
+      }
     }
   }
   if (!store || tok < 0 || tok >= a.total_tokens) return;
