@@ -52,7 +52,8 @@ def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed calls first (the GPU reaches its sustained clocks after ~100 ms of load)")
     ap.add_argument("--workload", default="mla_decode_b64_h128_k2048")
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
