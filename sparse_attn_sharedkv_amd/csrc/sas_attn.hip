@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   __shared__ __attribute__((aligned(8))) unsigned char flags[8];  // per-wave rescale votes
   __shared__ uint32_t rowid[RCHUNK];
   __shared__ uint32_t tmask[RCHUNK / TILE];
-  __shared__ int first_neg[2];  // first -1 of the top-k scan, per item parity
+  __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
