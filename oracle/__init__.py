@@ -1,8 +1,8 @@
 """CPU oracle for the sparse shared-KV attention decode path.
 
-TEST INFRASTRUCTURE ONLY. This package is the checker: only ``tests/``,
-``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import it. The product path (``sparse_attn_sharedkv_amd``) never imports,
+TEST INFRASTRUCTURE ONLY. This package is the oracle the parity tests check
+against: only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
+leg of ``bench.py`` may import it. The product path (``sparse_attn_sharedkv_amd``) never imports,
 links or calls anything here, and fails loudly when its HIP library is
 missing instead of falling back to this code.
 
@@ -14,7 +14,7 @@ Contents
 ``gen``         seeded input generators (paged pools, block tables, top-k
                 index sets) restating ``golden.py:315-473`` plus the
                 workload builders for the benchmark shapes.
-``checks``      the reference's tolerance checkers
+``checks``      the reference's tolerance rules as assertions
                 (``test_sparse_attn_sharedkv.py:394-481``) and the stricter
                 per-element bound used for this port.
 

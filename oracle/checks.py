@@ -1,4 +1,4 @@
-"""Tolerance checkers used by the parity tests.
+"""Tolerance rules used by the parity tests.
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
