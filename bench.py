@@ -131,7 +131,7 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
+        print("bench.py measures one MI355X: this library has no multi-GPU path "
               f"(asked for --gpus {args.gpus}, WORLD_SIZE={world})", file=sys.stderr)
         sys.exit(2)
 

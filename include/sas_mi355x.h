@@ -68,7 +68,7 @@ extern "C" {
 /* ---- error codes ---- */
 #define SAS_OK 0
 #define SAS_E_INVALID (-1)     /* bad argument (shape, pointer, scenario)      */
-#define SAS_E_UNSUPPORTED (-2) /* combination this build has no kernel for     */
+#define SAS_E_UNSUPPORTED (-2) /* combination this library has no kernel for   */
 #define SAS_E_CAPACITY (-3)    /* schedule does not fit the metadata capacity  */
 #define SAS_E_HIP (-4)         /* HIP runtime error (launch or attribute call) */
 
