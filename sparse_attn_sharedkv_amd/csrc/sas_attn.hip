@@ -780,11 +780,18 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
       //   barrier A(it): partials of tile it visible; stage (it + 2) % 3 (tile
       //                  it - 1's) free
       //   barrier B(it): P of tile it visible
-      // Tile it + 2 must have landed before barrier A(it + 1), where tile it + 3
-      // is issued into the stage tile it's P·V has just released.
+      // Tile it + 2 is issued at the head of iteration it, into the stage that
+      // barrier A(it) has released (tile it - 1's), and must have landed before
+      // barrier A(it + 1).
       write_partials(qk(0));
       __syncthreads();  // barrier A(0)
-      if (!FP8 && ntile > 2) issue(2, main_ptrs(2), rope_ptr(2));
+      // row addresses of the next tile to issue (tile it + 2 at the head of
+      // iteration it; garbage and unused when there is no such tile)
+      uint64_t pend_main = 0, pend_rope = 0;
+      if constexpr (!FP8) {
+        pend_main = main_ptrs(2);
+        pend_rope = rope_ptr(2);
+      }
 
       for (int it = 0; it < ntile; ++it) {
         const int stage = it % NSTAGE;
@@ -847,6 +854,11 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           xp[1] = ds_read_b128_asm<1024>(xa);
           xp[2] = ds_read_b128_asm<2048>(xa);
           xp[3] = ds_read_b128_asm<3072>(xa);
+          // Tile it + 2 into the stage tile it - 1 has released (barrier A(it)),
+          // issued behind this phase's first LDS reads so that their latency runs
+          // under the DMA issue's memory-pipeline back-pressure. The LDS DMA
+          // counts in vmcnt only: the lgkmcnt waits below are unchanged.
+          if (it + 2 < ntile) issue((it + 2) % NSTAGE, pend_main, pend_rope);
           // mask, row ids and Kᵀ have landed (only the four partial reads may be
           // pending; LDS reads of a wave complete in order). Each asm output
           // register appears once: a duplicated operand makes the compiler copy
@@ -979,7 +991,10 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           if (!FP8) write_partials(st_next);
           if (!FP8) wait_vmcnt<0>();  // this wave's share of tile it + 2 has landed
           __syncthreads();            // barrier A(it + 1)
-          if (!FP8 && it + 3 < ntile) issue((it + 3) % NSTAGE, nx_main, nx_rope);
+          if constexpr (!FP8) {       // tile it + 3 is issued at the next loop head
+            pend_main = nx_main;
+            pend_rope = nx_rope;
+          }
         }
       }
       __syncthreads();  // rowid / tmask / ring are rewritten by the next chunk or item
