@@ -41,7 +41,7 @@ FD_M_NUM_INDEX = 6
 DEFAULT_CORE_NUM = 256
 DEFAULT_S2_BASE = 64          # positions per schedulable block
 DEFAULT_MIN_SPLIT_BLOCKS = 2  # never split an item into pieces shorter than 128 positions
-DEFAULT_FD_HEAD_CHUNK = 32    # heads per merge task
+DEFAULT_FD_HEAD_CHUNK = 64    # heads per merge task (a whole 64-head item)
 
 
 def m_base_for(num_heads: int) -> int:

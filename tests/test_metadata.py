@@ -183,8 +183,9 @@ def test_benchmark_workload_schedules(name):
     cfg = _check_schedule(md, [w["S"]] * w["B"], lens, w["H"], w["window"], scen,
                           w["cmp_ratio"] or 1, w["K"], M.DEFAULT_CORE_NUM)
     if name == "mla_decode_b64_h128_k2048":
-        # 64 tokens x 2 head blocks, each split in two: one workgroup per CU
-        assert cfg["num_fa"] == 256 and cfg["num_fd"] == 256
+        # 64 tokens x 2 head blocks, each split in two: one workgroup per CU,
+        # one merge task per 64-head item
+        assert cfg["num_fa"] == 256 and cfg["num_fd"] == 128
 
 
 def test_ragged_and_empty_items():
