@@ -24,6 +24,7 @@ test_gpu_parity.py.
 """
 
 import math
+import os
 import sys
 
 import numpy as np
@@ -42,7 +43,7 @@ requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
 if HAS_GPU:
     from sparse_attn_sharedkv_amd import sparse_attn_sharedkv, sparse_attn_sharedkv_metadata
 
-N_CASES = 40
+N_CASES = int(os.environ.get("SAS_SWEEP_CASES", "40"))  # more for a longer validation run
 
 
 def _say(msg):
