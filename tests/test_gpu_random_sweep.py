@@ -44,6 +44,7 @@ if HAS_GPU:
     from sparse_attn_sharedkv_amd import sparse_attn_sharedkv, sparse_attn_sharedkv_metadata
 
 N_CASES = int(os.environ.get("SAS_SWEEP_CASES", "40"))  # more for a longer validation run
+DTYPE = {"bf16": torch.bfloat16, "fp16": torch.float16}[os.environ.get("SAS_SWEEP_DTYPE", "bf16")]
 
 
 def _say(msg):
@@ -92,7 +93,7 @@ def test_random_configuration(i):
          f"q={cfg['cu_seqlens_q']} kv={cfg['seqused_kv']} H={cfg['N1']} "
          f"win={cfg['ori_win_left']} ratio={cfg['cmp_ratio']} K={cfg['K']} "
          f"blocks={cfg['block_size1']}/{cfg['block_size2']} cores={cfg['cores']}")
-    kw = gen.build_case(cfg, torch.bfloat16, seed=2000 + i)
+    kw = gen.build_case(cfg, DTYPE, seed=2000 + i)
     cu = torch.tensor(cfg["cu_seqlens_q"], dtype=torch.int32)
     md = sparse_attn_sharedkv_metadata(
         num_heads_q=cfg["N1"], num_heads_kv=1, head_dim=cfg["D"],
