@@ -15,6 +15,7 @@
   turns every output into NaN instead of leaving stale memory.
 """
 
+import os
 import sys
 
 import numpy as np
@@ -73,7 +74,7 @@ def _random_cases(seed=0, n=60):
 
 @requires_gpu
 def test_device_schedule_equals_host_schedule_word_for_word():
-    cases = _random_cases()
+    cases = _random_cases(n=int(os.environ.get("SAS_SCHED_CASES", "60")))  # more for a longer run
     for i, c in enumerate(cases):
         _say(f"case {i}: batch={len(c['act_q'])} heads={c['num_heads']} "
              f"scenario={c['scenario']} cores={c['core_num']}")
