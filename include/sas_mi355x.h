@@ -52,7 +52,8 @@ extern "C" {
  * fd_head_chunk, 0, 0, 0, query rows of each batch..., block count of each item...];
  * word 0 is 0 when the inputs do not fit the key region. The device scheduler
  * leaves a buffer that already holds the key of its inputs (and a valid config
- * row) as it is: the schedule is a function of exactly these words.
+ * row) as it is when called with reuse != 0: the schedule is a function of exactly
+ * these words. Pass reuse != 0 only for a buffer that nothing else writes between calls.
  */
 #define SAS_AIC_CORE_NUM 512
 #define SAS_AIV_CORE_NUM 1024
@@ -98,6 +99,10 @@ int sas_metadata_build(int32_t* meta_out, int batch, const int32_t* act_q,
  * <= SAS_DEV_SCHED_MAX_ITEMS. Errors the host cannot see (a negative length, too many
  * items, a schedule over capacity) leave the config row without SAS_META_MAGIC and
  * its word 1 = -1 / -2 / -3; sas_attention_launch then writes NaN outputs.
+ * reuse: 0 always rebuilds meta; nonzero keeps it when it already holds the schedule key
+ * of these inputs and a valid config row (about 5 us instead of a full rebuild), which is
+ * only sound for a buffer that the caller owns and nothing else writes between calls
+ * (a captured graph's static buffer, a per-stream buffer kept for the purpose).
  * Asynchronous; returns SAS_E_INVALID for arguments checkable on the host. */
 #define SAS_DEV_SCHED_MAX_BATCH 4096
 #define SAS_DEV_SCHED_MAX_ITEMS 16384
@@ -105,7 +110,7 @@ int sas_metadata_build_device(int32_t* meta, int batch, const int32_t* act_q,
                               int uniform_q, const int32_t* seqused_kv, int num_heads,
                               int m_base, int ori_win_left, int scenario, int cmp_ratio,
                               int cmp_topk, int num_cores, int s2_base, int min_split_blocks,
-                              int fd_head_chunk, void* stream);
+                              int fd_head_chunk, int reuse, void* stream);
 
 /* Bytes of split-KV partial workspace for a schedule:
  * num_partial_slots * m_base * (head_dim_v + 1) * sizeof(float). */

@@ -106,7 +106,7 @@ def load() -> ctypes.CDLL:
         lib.sas_metadata_build_device.restype = ctypes.c_int
         lib.sas_metadata_build_device.argtypes = ([ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                                                    ctypes.c_int, ctypes.c_void_p] +
-                                                  [ctypes.c_int] * 10 + [ctypes.c_void_p])
+                                                  [ctypes.c_int] * 11 + [ctypes.c_void_p])
         lib.sas_workspace_bytes.restype = ctypes.c_int64
         lib.sas_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.sas_attention_launch.restype = ctypes.c_int

@@ -26,13 +26,15 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import threading
 from dataclasses import dataclass, field
 from typing import Optional, Tuple, Union
 
 import torch
 
 from . import _lib
-from .metadata import (DEFAULT_CORE_NUM, DEFAULT_S2_BASE, SAS_META_SIZE,  # noqa: F401
+from .metadata import (AIC_CORE_NUM, DEFAULT_CORE_NUM, DEFAULT_S2_BASE,  # noqa: F401
+                       SAS_META_SIZE,
                        build_metadata, build_metadata_device, config_row, m_base_for)
 
 DEFAULT_BLOCK_I = 128  # kernel.py:65, kept for callers that import it
@@ -80,6 +82,25 @@ def _cached_schedule(act_q: tuple, act_kv: tuple, num_heads: int, ori_win_left: 
                           cmp_topk=topk, core_num=core_num)
 
 
+# Schedules built by the on-device scheduler for calls without ``metadata``: one
+# library-owned buffer per (device, stream), written only by that scheduler on
+# that stream, so an unchanged schedule is kept instead of rebuilt. Calls on one
+# stream run in order; different streams get different buffers.
+_DEVICE_SCHEDULES: dict = {}
+_DEVICE_SCHEDULES_LOCK = threading.Lock()
+
+
+def _schedule_buffer(dev: torch.device) -> torch.Tensor:
+    st = torch.cuda.current_stream(dev)
+    key = (dev.index, st.cuda_stream)
+    with _DEVICE_SCHEDULES_LOCK:
+        buf = _DEVICE_SCHEDULES.get(key)
+        if buf is None:
+            buf = torch.zeros(SAS_META_SIZE, dtype=torch.int32, device=dev)
+            _DEVICE_SCHEDULES[key] = buf
+    return buf
+
+
 def _ptr(t: Optional[torch.Tensor]):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
@@ -96,14 +117,18 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             core_num: int = DEFAULT_CORE_NUM, topk_cmp: Optional[int] = None,
             head_dim_v: Optional[int] = None,
             kv_cache_dtype: Optional[str] = None,
-            schedule: Optional[str] = None) -> Prepared:
+            schedule: Optional[str] = None,
+            _stream_schedule: bool = False) -> Prepared:
     """Validate and stage one call (host work of api.py:186-384) without launching.
 
     ``schedule``: ``"host"`` reads the lengths back and schedules on the CPU (the
     reference's behaviour, api.py:335-360); ``"device"`` keeps them on the GPU and
     runs the on-device scheduler (no host synchronisation); ``None`` means
     ``"device"`` when ``metadata`` is a GPU tensor (it is then not read back) and
-    ``"host"`` otherwise.
+    ``"host"`` otherwise. ``_stream_schedule`` (for callers that launch right after
+    preparing, on the same stream): a device-built schedule goes to the library's
+    buffer for the current stream and is kept when unchanged; otherwise every
+    prepared call schedules into a buffer of its own.
     """
     del seqused_q  # API-parity placeholder (api.py:186)
     assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
@@ -208,6 +233,15 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     if metadata is not None:
         assert metadata.numel() == SAS_META_SIZE, (
             f"metadata must have {SAS_META_SIZE} int32 entries (got {metadata.numel()})")
+    # the kernels read seqused_kv[b] and block-table row b for every batch b
+    if seqused_kv.numel() < nb:
+        raise ValueError(f"seqused_kv has {seqused_kv.numel()} entries for {nb} sequences")
+    if ori_block_table.dim() != 2 or ori_block_table.shape[0] < nb:
+        raise ValueError(f"ori_block_table must be [>= {nb}, table_len] "
+                         f"(got {tuple(ori_block_table.shape)})")
+    if scenario >= 2 and (cmp_block_table.dim() != 2 or cmp_block_table.shape[0] < nb):
+        raise ValueError(f"cmp_block_table must be [>= {nb}, table_len] "
+                         f"(got {tuple(cmp_block_table.shape)})")
 
     dev = q.device
     if dev.type != "cuda":
@@ -233,13 +267,18 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             metadata_dev = build_metadata_device(
                 batch=nb, act_q=act_q_d, act_kv=seqused, num_heads=int(n1),
                 ori_win_left=int(ori_win_left), scenario=scenario, cmp_ratio=cmp_ratio_eff,
-                cmp_topk=int(k), core_num=int(core_num))
+                cmp_topk=int(k), core_num=int(core_num),
+                out=_schedule_buffer(dev) if _stream_schedule else None)
         else:
             metadata_dev = metadata.to(device=dev, dtype=i32).reshape(SAS_META_SIZE).contiguous()
-        # capacities; the kernels read the schedule's own summary on the GPU
-        cfg = dict(num_fa=int(core_num), num_fd=_lib.SCHED_DEVICE,
-                   num_partial_slots=2 * int(core_num), s2_base=DEFAULT_S2_BASE,
-                   m_base=m_base_for(n1))
+        # capacities; the kernels read the schedule's own summary on the GPU. A
+        # schedule supplied on the GPU may have been built for any core count up to
+        # AIC_CORE_NUM, which this call cannot read without a host sync: launch for
+        # that many workgroups (the unused ones exit at once) and size the workspace
+        # for the most partial pieces such a schedule can have (two per core).
+        cap = int(core_num) if metadata is None else AIC_CORE_NUM
+        cfg = dict(num_fa=cap, num_fd=_lib.SCHED_DEVICE, num_partial_slots=2 * cap,
+                   s2_base=DEFAULT_S2_BASE, m_base=m_base_for(n1))
     elif metadata is None:
         kv_host = tuple(int(x) for x in seqused_kv.to(torch.int32).cpu().tolist())
         md = _cached_schedule(tuple(act_q), kv_host, int(n1), int(ori_win_left), scenario,
@@ -376,6 +415,6 @@ def sparse_attn_sharedkv(
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
                    core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
-                   kv_cache_dtype=kv_cache_dtype, schedule=schedule)
+                   kv_cache_dtype=kv_cache_dtype, schedule=schedule, _stream_schedule=True)
     launch(prep)
     return finalize(prep, return_softmax_lse)

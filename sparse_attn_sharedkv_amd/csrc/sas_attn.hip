@@ -533,12 +533,11 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         }
         if (mine < g.n_cmp) atomicMin(&first_neg[item_par], mine);
       }
-      // Block-table words, then (first chunk) the query fragment. d_qk 512: as
-      // asm loads with exact counts, so the table words are waited for with the
-      // NKS query loads still in flight (they land with the first tiles); every
-      // load has an in-bounds address (masked lanes read word 0 of the window
-      // table). d_qk 576 has no registers to spare for that and loads the query
-      // after the resolution.
+      // Block-table words (the query fragment is loaded after the resolution).
+      // d_qk 512: as asm loads with one wait, the wait and the tie of their
+      // destination registers being one statement (no copy of a register can be
+      // placed between an asm load and its wait); every load has an in-bounds
+      // address (masked lanes read word 0 of the window table).
       const bool load_q = c0 == p_lo;
       if constexpr (!ROPE) {
         bool tab_ok[PER];
@@ -558,23 +557,12 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           const int32_t* src = tab_ok[e] ? tbl + (size_t)b * tlen + bi : a.ori_block_table;
           asm volatile("global_load_dword %0, %1, off" : "=v"(tword[e]) : "v"(src) : "memory");
         }
-        if (load_q) {
-          const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
-                                                   (head_ok ? head : 0)) * DQK;
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            const short* src = qrow + 128 * q + 16 * ks + 8 * hl;
-            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qf[ks]) : "v"(src) : "memory");
-          }
-          wait_vmcnt<NKS>();
-        } else {
-          wait_vmcnt<0>();
-        }
         static_assert(PER == 2 || PER == 4, "resolution positions per thread");
         if constexpr (PER == 2)
-          asm volatile("" : "+v"(tword[0]), "+v"(tword[1]) : : "memory");
+          asm volatile("s_waitcnt vmcnt(0)" : "+v"(tword[0]), "+v"(tword[1]) : : "memory");
         else
-          asm volatile("" : "+v"(tword[0]), "+v"(tword[1]), "+v"(tword[2]), "+v"(tword[3])
+          asm volatile("s_waitcnt vmcnt(0)"
+                       : "+v"(tword[0]), "+v"(tword[1]), "+v"(tword[2]), "+v"(tword[3])
                        : : "memory");
 #pragma unroll
         for (int e = 0; e < PER; ++e) tab[e] = tab_ok[e] ? tword[e] : -1;
@@ -716,33 +704,21 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         issue(0, main_ptrs(0), rope_ptr(0));
         if (ntile > 1) issue(1, main_ptrs(1), rope_ptr(1));
       }
-      if constexpr (ROPE) {
-        if (load_q) {
-          const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
-                                                   (head_ok ? head : 0)) * DQK;
+      // query fragment (compiler-visible loads, in flight with tiles 0 and 1)
+      if (load_q) {
+        const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
+                                                 (head_ok ? head : 0)) * DQK;
 #pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            const int dim = ks < NKS_MAIN ? (128 * q + 16 * ks + 8 * hl) : (512 + 16 * q + 8 * hl);
-            i16x8 v = *(const i16x8*)(qrow + dim);
-            qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
-          }
+        for (int ks = 0; ks < NKS; ++ks) {
+          const int dim = ks < NKS_MAIN ? (128 * q + 16 * ks + 8 * hl) : (512 + 16 * q + 8 * hl);
+          i16x8 v = *(const i16x8*)(qrow + dim);
+          qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
         }
       }
       // A wait the compiler can see: it clears its pending-load state here, so it
       // puts no vmcnt wait for qf inside the tile loop (that wait would also drain
       // the row DMAs in flight on every tile). Also lands tiles 0 and 1.
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
-      if constexpr (!ROPE) {
-        if (load_q) {  // the asm query loads have landed; zero the fragment of absent rows
-          static_assert(NKS == 8, "query k-steps");
-          asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]),
-                       "+v"(qf[5]), "+v"(qf[6]), "+v"(qf[7]) : : "memory");
-          if (!(head_ok && tok_ok)) {
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[ks] = (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
-          }
-        }
-      }
       if (FP8 && ntile > 2) fp8_load(fpt, main_ptrs(2));
       __syncthreads();
 

@@ -155,6 +155,7 @@ struct Params {
   const int32_t* seqused_kv;    // [batch]
   int32_t batch, uniform_q, num_heads, m_base, ori_win_left, scenario, cmp_ratio, cmp_topk;
   int32_t num_cores, s2_base, min_split_blocks, fd_head_chunk;
+  int32_t reuse;  // nonzero: a buffer already holding this schedule's key is kept
 };
 
 constexpr int BPT = (SAS_DEV_SCHED_MAX_BATCH + NT - 1) / NT;  // batches per thread in the prefix
@@ -263,6 +264,10 @@ __global__ __launch_bounds__(NT) void sched_kernel(const Params p) {
   __syncthreads();
 
   // ---- the buffer already holds the schedule of these inputs: keep it ----
+  // Only for a buffer its owner declares persistent (p.reuse): one that nothing
+  // but this scheduler writes between calls, such as a captured graph's static
+  // buffer. A freshly allocated buffer may hold a stale key and config row over
+  // rows that something else has since overwritten, so it is always rebuilt.
   const int keyw = 16 + batch + n;  // key words
   const bool keyable = keyw <= SAS_CFG_OFFSET - SAS_META_KEY_OFFSET;
   auto key_word = [&](int w) -> int32_t {
@@ -273,7 +278,7 @@ __global__ __launch_bounds__(NT) void sched_kernel(const Params p) {
                              p.s2_base, p.min_split_blocks, p.fd_head_chunk, 0, 0, 0};
     return hdr[w];
   };
-  if (keyable) {
+  if (keyable && p.reuse) {
     bool miss = tid == 0 && cfg[0] != SAS_META_MAGIC;
     for (int w = tid; w < keyw; w += NT) miss = miss || key[w] != key_word(w);
     if (miss) s_miss = 1;
@@ -478,7 +483,8 @@ extern "C" int sas_metadata_build_device(int32_t* meta, int batch, const int32_t
                                          int uniform_q, const int32_t* seqused_kv, int num_heads,
                                          int m_base, int ori_win_left, int scenario, int cmp_ratio,
                                          int cmp_topk, int num_cores, int s2_base,
-                                         int min_split_blocks, int fd_head_chunk, void* stream) {
+                                         int min_split_blocks, int fd_head_chunk, int reuse,
+                                         void* stream) {
   if (!meta || batch < 0 || batch > SAS_DEV_SCHED_MAX_BATCH || (batch > 0 && !seqused_kv) ||
       (!act_q && uniform_q < 0)) {
     sas::set_error("sas_metadata_build_device: null pointer or batch out of range");
@@ -507,6 +513,7 @@ extern "C" int sas_metadata_build_device(int32_t* meta, int batch, const int32_t
   p.s2_base = s2_base;
   p.min_split_blocks = min_split_blocks;
   p.fd_head_chunk = fd_head_chunk;
+  p.reuse = reuse != 0;
   hipLaunchKernelGGL(sasdev::sched_kernel, dim3(1), dim3(sasdev::NT), 0, (hipStream_t)stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -151,7 +151,8 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
                           s2_base: int = DEFAULT_S2_BASE,
                           min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
                           fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK,
-                          stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+                          stream: Optional[torch.cuda.Stream] = None,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Run the on-device scheduler (``sas_metadata_build_device``) on the current stream.
 
     ``act_q`` / ``act_kv``: int32 ``[batch]`` tensors on the GPU (``act_q`` None: every
@@ -159,6 +160,11 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
     the same GPU, word for word what ``build_metadata`` returns for the same lengths;
     nothing is read back. Lengths the host cannot check (negative, too many items) leave
     a schedule the attention launch turns into NaN outputs.
+
+    ``out``: a persistent int32 ``[SAS_META_SIZE]`` buffer owned by the caller, which
+    nothing else writes between calls. The schedule is written there, and when the
+    buffer already holds the schedule of these inputs it is kept (a few microseconds
+    instead of a rebuild). Without ``out`` a new buffer is allocated and always built.
     """
     lib = _lib.load()
     dev = act_kv.device
@@ -170,14 +176,20 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
         if t is not None and (t.dtype != torch.int32 or t.device != dev or t.numel() < batch
                               or not t.is_contiguous()):
             raise ValueError("act_q / act_kv must be contiguous int32 [batch] tensors on one GPU")
-    out = torch.empty(SAS_META_SIZE, dtype=torch.int32, device=dev)
+    reuse = out is not None
+    if out is None:
+        out = torch.empty(SAS_META_SIZE, dtype=torch.int32, device=dev)
+    elif (out.dtype != torch.int32 or out.device != dev or out.numel() != SAS_META_SIZE
+          or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous int32 [{SAS_META_SIZE}] tensor on {dev}")
     st = stream if stream is not None else torch.cuda.current_stream(dev)
     rc = lib.sas_metadata_build_device(
         ctypes.c_void_p(out.data_ptr()), int(batch),
         ctypes.c_void_p(act_q.data_ptr() if act_q is not None else 0), int(uniform_q),
         ctypes.c_void_p(act_kv.data_ptr()), int(num_heads), m_base_for(int(num_heads)),
         int(ori_win_left), int(scenario), int(cmp_ratio), int(cmp_topk), int(core_num),
-        int(s2_base), int(min_split_blocks), int(fd_head_chunk), ctypes.c_void_p(st.cuda_stream))
+        int(s2_base), int(min_split_blocks), int(fd_head_chunk), int(reuse),
+        ctypes.c_void_p(st.cuda_stream))
     if rc < 0:
         raise ValueError(_lib.last_error())
     return out

@@ -53,6 +53,6 @@ def sparse_flash_mla(
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
                    core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
-                   kv_cache_dtype=kv_cache_dtype, schedule=schedule)
+                   kv_cache_dtype=kv_cache_dtype, schedule=schedule, _stream_schedule=True)
     launch(prep)
     return finalize(prep, return_softmax_lse)

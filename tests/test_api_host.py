@@ -105,3 +105,16 @@ def test_fp8_cache_gates():
     kv = torch.zeros(4, 64, 1, 656, dtype=torch.bfloat16)  # bf16 tensor named fp8
     with pytest.raises(ValueError):
         sparse_flash_mla(**_fp8_call(ori_kv=kv, cmp_kv=kv), kv_cache_dtype="fp8_ds_mla")
+
+
+def test_short_length_and_table_tensors(swa_case, scfa_case):
+    # the kernels read seqused_kv[b] and table row b for every sequence b: a shorter
+    # tensor is rejected on the host before anything reaches the device
+    nb = swa_case["cu_seqlens_q"].numel() - 1
+    with pytest.raises(ValueError):
+        sparse_attn_sharedkv(**dict(swa_case, seqused_kv=swa_case["seqused_kv"][: nb - 1]))
+    with pytest.raises(ValueError):
+        sparse_attn_sharedkv(**dict(swa_case, ori_block_table=swa_case["ori_block_table"][: nb - 1]))
+    with pytest.raises(ValueError):
+        sparse_attn_sharedkv(**dict(scfa_case,
+                                    cmp_block_table=scfa_case["cmp_block_table"][: nb - 1]))

@@ -71,7 +71,7 @@ def test_device_scheduler_rejects_bad_arguments_without_a_gpu():
         return lib.sas_metadata_build_device(meta, batch, act_q, uniform_q, act_kv,
                                              a["num_heads"], a["m_base"], a["win"], a["scenario"],
                                              a["ratio"], a["topk"], a["cores"], a["s2"], a["split"],
-                                             a["chunk"], None)
+                                             a["chunk"], 0, None)
 
     assert call(meta=None) == -1
     assert call(batch=_lib.DEV_SCHED_MAX_BATCH + 1) == -1
