@@ -270,15 +270,18 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
                        ori_win_right: int = 0, layout_q: str = "TND",
                        head_dim_v: Optional[int] = None,
                        tokens: Optional[Sequence[int]] = None,
-                       kv_cache_dtype: Optional[str] = None):
+                       kv_cache_dtype: Optional[str] = None, attend=None):
     """Golden output of ``sparse_attn_sharedkv`` for the API's own tensors.
 
     Returns ``(out, lse)`` in the caller's layout (``[T, N1, Dv]``/``[T, N1]``
     for TND, ``[B, S, N1, Dv]``/``[B, S, N1]`` for BSND); padded query rows
     stay zero (golden.py:106-111). ``tokens`` restricts the work to a subset
     of flat token ids (others stay zero) so large workloads can be sampled.
-    All tensors are read on the CPU.
+    ``attend`` replaces the per-token math (default ``attend_token``; the
+    kernel-order restatement of ``kernel_order`` plugs in here). All tensors
+    are read on the CPU.
     """
+    attend = attend_token if attend is None else attend
     q = q.cpu()
     n1, d = q.shape[-2], q.shape[-1]
     dv = d if head_dim_v is None else int(head_dim_v)
@@ -309,7 +312,7 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
                 cmp_idx_row=None if idx_flat is None else idx_flat[t, 0].tolist(),
                 cmp_ratio=cmp_ratio, ori_win_left=ori_win_left, ori_win_right=ori_win_right,
                 kv_cache_dtype=kv_cache_dtype)
-            o, l = attend_token(q_flat[t], [ori_rows, cmp_rows], sinks, softmax_scale, d_v=dv)
+            o, l = attend(q_flat[t], [ori_rows, cmp_rows], sinks, softmax_scale, d_v=dv)
             out[t] = o
             lse[t] = l
     if layout_q == "TND":

@@ -1,0 +1,98 @@
+"""Agreement with golden of the kernel's rounding order, per lazy-rescale threshold.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): a CPU study, no GPU.
+
+For each random configuration of the GPU sweep (``gen.random_sweep_cfg``, the
+reference's U(-10, 10) inputs) it computes golden (``golden_ref``, 512-row
+tiles), the float64 closed form, golden with 32-row tiles, and the kernel's
+order (``kernel_order``) for several thresholds ``tau`` and stream counts, and
+reports per variant how many configurations fail the reference's rule
+(>= 99.5 % of elements within rtol 2^-7 / atol 1e-4 of golden) and how many
+have elements beyond atol = rtol = 2e-2 of golden.
+
+    python -m oracle.rescale_study --cases 300 --jobs 8 [--json out.json]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import sys
+from multiprocessing import Pool
+
+import numpy as np
+import torch
+
+from . import gen
+from .golden_ref import attend_token, sparse_attn_exact, sparse_attn_oracle
+from .kernel_order import compare, sparse_attn_kernel_order
+
+# (name, tile, tau, streams); "golden32" is golden's own algorithm at 32-row tiles
+VARIANTS = [("golden32", 32, None, 1)] + [(f"tau{t}", 32, float(t), 1) for t in (0, 1, 2, 4, 8)] + \
+           [("tau0_s2", 32, 0.0, 2), ("tau8_s2", 32, 8.0, 2)]
+
+
+def run_case(i: int) -> dict:
+    torch.set_num_threads(1)
+    cfg = gen.random_sweep_cfg(np.random.default_rng(1000 + i))
+    kw = gen.build_case(cfg, torch.bfloat16, seed=2000 + i)
+    kw.pop("topk_cmp", None)
+    ref, _ = sparse_attn_oracle(**kw)
+    ex, _ = sparse_attn_exact(**kw)
+    res = dict(case=i, scenario=cfg["scenario"], heads=cfg["N1"])
+    for name, tile, tau, streams in VARIANTS:
+        if tau is None:
+            def g32(qt, segments, sinks, scale, d_v=None):
+                return attend_token(qt, segments, sinks, scale, d_v=d_v, tile=tile)
+            x, _ = sparse_attn_oracle(attend=g32, **kw)
+        else:
+            x, _ = sparse_attn_kernel_order(tile=tile, tau=tau, streams=streams, **kw)
+        res[name] = compare(x, ref, ex)
+    return res
+
+
+def summarize(rows: list) -> dict:
+    out = {}
+    for name, *_ in VARIANTS:
+        v = [r[name] for r in rows]
+        pct = np.array([x["pct_ref"] for x in v])
+        beyond = np.array([x["beyond_2e2"] for x in v])
+        ratio = np.array([x["err_exact"] / max(x["golden_exact"], 1e-30) for x in v])
+        out[name] = dict(cases=len(v), under_99_5=int((pct < 99.5).sum()), min_pct=float(pct.min()),
+                         median_pct=float(np.median(pct)), with_beyond_2e2=int((beyond > 0).sum()),
+                         max_beyond_2e2=int(beyond.max()),
+                         max_abs=float(max(x["max_abs"] for x in v)),
+                         median_ratio_exact=float(np.median(ratio)), max_ratio_exact=float(ratio.max()))
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--cases", type=int, default=300)
+    ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--json", default=None)
+    args = ap.parse_args(argv)
+    with Pool(args.jobs) as pool:
+        rows = []
+        for r in pool.imap_unordered(run_case, range(args.cases)):
+            rows.append(r)
+            if len(rows) % 25 == 0:
+                print(f"{len(rows)} / {args.cases} cases", flush=True)
+    rows.sort(key=lambda r: r["case"])
+    summ = summarize(rows)
+    hdr = f"{'variant':10s} {'<99.5%':>7s} {'min %':>8s} {'med %':>8s} {'>2e-2':>6s} " \
+          f"{'max n':>6s} {'max|d|':>8s} {'med r':>6s} {'max r':>6s}"
+    print(hdr)
+    for name, s in summ.items():
+        print(f"{name:10s} {s['under_99_5']:7d} {s['min_pct']:8.3f} {s['median_pct']:8.3f} "
+              f"{s['with_beyond_2e2']:6d} {s['max_beyond_2e2']:6d} {s['max_abs']:8.4f} "
+              f"{s['median_ratio_exact']:6.2f} {s['max_ratio_exact']:6.2f}")
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump(dict(summary=summ, cases=rows), f)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

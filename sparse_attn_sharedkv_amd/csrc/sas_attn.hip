@@ -5,30 +5,30 @@
 // with one metadata-driven HIP kernel plus a split-KV merge kernel.
 //
 // Work decomposition
-//   One workgroup per FA metadata row; it walks its items (query rows) and,
-//   inside each, its blocks of the attended list [window rows ++ compressed
-//   positions]. All query heads of a token share every gathered KV row
-//   (shared KV, N2 = 1): a 32-row tile is loaded once into LDS and read by
-//   every wave, as K for Q·Kᵀ and (first head_dim_v columns) as V for P·V.
+//   One workgroup per FA metadata row; it walks its items (query row x 32- or
+//   64-head m-block) and, inside each, its blocks of the attended list [window
+//   rows ++ compressed positions]. All query heads of a token share every
+//   gathered KV row (shared KV, N2 = 1): a 32-row tile is loaded once into LDS
+//   and read by every wave, as K for Q·Kᵀ and (first head_dim_v columns) as V
+//   for P·V.
 //
-// Waves (NHG head groups of 32 heads x 4 dims quarters = 4*NHG waves, two per
-// SIMD for the 64-head items of H > 32; details at attn_kernel):
-//   Q·Kᵀ: each wave computes a partial Sᵀ[32 rows x 32 heads] over its quarter
-//         of d_qk with v_mfma_f32_32x32x16 (A = K rows from LDS, B = Qᵀ held in
-//         VGPRs); the four partials of a head group are summed through LDS.
-//   softmax: exp2 domain on 4 rows x 1 head per lane; P shared through LDS;
-//         lazy rescaling (the O rescale only runs when some head's max grows
-//         by more than 2^8).
-//   P·V:  each wave accumulates Oᵀ[its dv quarter x 32 heads] (A = Vᵀ via
-//         ds_read_b64_tr_b16 from the row-major tile, B = Pᵀ from LDS).
-//   The tile loop is software-pipelined: Q·Kᵀ of the next tile is issued
-//   before the softmax of this one, so the two overlap.
+// Waves (one per SIMD; details at attn2_kernel): head groups of 32 heads x 2
+// halves of d_qk / d_v.
+//   Q·Kᵀ: each wave computes a partial Sᵀ[32 rows x 32 heads] over its half of
+//         d_qk with v_mfma_f32_32x32x16 (A = K rows from LDS, B = Qᵀ held in
+//         AGPRs); the two partials of a head group meet through LDS, so both
+//         waves hold the same full Sᵀ.
+//   softmax: exp2 domain on 16 rows x 1 head per lane, in registers; the
+//         running max moves at every tile whose max exceeds it.
+//   P·V:  each wave accumulates Oᵀ[its dv half x 32 heads] (A = Vᵀ via
+//         ds_read_b64_tr_b16 from the row-major tile, B = Pᵀ straight from the
+//         Sᵀ registers).
 //
 // Gather: global_load_lds_dwordx4 (16 B per lane straight into LDS, no VGPR
-//   staging) into a 3-stage ring; rows of a tile are rotated by 16-byte
-//   chunks so both the Kᵀ reads (b128) and the transposed V reads (tr_b16)
-//   are bank-conflict free. fp8 cache rows are loaded into VGPRs instead and
-//   dequantized into the same bf16 layout.
+//   staging) into a 3-stage ring, issued between the Q·Kᵀ MFMAs; rows of a
+//   tile are rotated by 16-byte chunks so both the Kᵀ reads (b128) and the
+//   transposed V reads (tr_b16) are bank-conflict free. fp8 cache rows are
+//   loaded into VGPRs instead and dequantized into the same bf16 layout.
 //
 // Numerics follow golden.py:156-200: fp32 scores, P rounded to the input
 // dtype before P·V while the running sum uses fp32 P, out = acc / l rounded
@@ -40,6 +40,7 @@
 #include <string.h>
 
 #include <string>
+#include <type_traits>
 
 #include "../../include/sas_mi355x.h"
 #include "sas_items.h"
@@ -60,12 +61,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define SAS_GLOBAL __attribute__((address_space(1)))
 
 constexpr int TILE = 32;        // KV rows per pipeline stage
-constexpr int NSTAGE = 3;       // LDS ring depth
-constexpr int RCHUNK = 1024;    // positions resolved into LDS at a time
 constexpr uint32_t ROW_INVALID = 0xFFFFFFFFu;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
-constexpr float RESCALE_TAU = 8.0f;  // lazy-rescale threshold (log2 units)
+#ifndef SAS_KPF
+#define SAS_KPF 8  // K operand reads in flight per wave (attn2_kernel)
+#endif
+#ifndef SAS_VPF
+#define SAS_VPF 4  // Vᵀ operands in flight per wave (attn2_kernel)
+#endif
 
 template <typename T> struct MfmaOps;
 template <> struct MfmaOps<__bf16> {
@@ -155,59 +159,9 @@ __device__ inline int32_t ld_uniform(const int32_t* p) {
   return *(const __attribute__((address_space(4))) int32_t*)p;
 }
 
-// Materialise a value at this point of the program: the empty asm (ordered
-// with the barriers and the DMA asm) consumes it, so its computation cannot be
-// sunk past the next barrier towards its use.
-__device__ inline void pin_u64(uint64_t& v) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  asm volatile("" : "+v"(lo), "+v"(hi));
-  v = ((uint64_t)hi << 32) | lo;
-}
-
 template <int N>
 __device__ inline void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// ds_read_b64_tr_b16 with an immediate offset (the builtin does not fold
-// offsets, which costs one address VGPR per read). The result is not tracked
-// by the compiler's lgkmcnt bookkeeping: consume it only after lds_wait_pv.
-template <int OFF>
-__device__ inline i16x4 ds_read_tr16(uint32_t addr) {
-  i16x4 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
-  return v;
-}
-
-template <int OFF>
-__device__ inline i16x8 ds_read_b128_asm(uint32_t addr) {
-  i16x8 v;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
-  return v;
-}
-__device__ inline uint32_t ds_read_b32_asm(uint32_t addr) {
-  uint32_t v;
-  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr) : "memory");
-  return v;
-}
-__device__ inline uint64_t ds_read_b64_asm(uint32_t addr) {
-  uint64_t v;
-  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr) : "memory");
-  return v;
-}
-
-// Wait for every LDS operation of this wave; all registers written by the
-// untracked asm reads pass through the asm, so no consumer (and no copy) of
-// them can be placed above the wait.
-__device__ inline void lds_wait_pv(uint64_t& votes, i16x8 (&p)[2], i16x4 (&g0)[8],
-                                   i16x4 (&g1)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(votes), "+v"(p[0]), "+v"(p[1]), "+v"(g0[0]), "+v"(g0[1]), "+v"(g0[2]),
-                 "+v"(g0[3]), "+v"(g0[4]), "+v"(g0[5]), "+v"(g0[6]), "+v"(g0[7]), "+v"(g1[0]),
-                 "+v"(g1[1]), "+v"(g1[2]), "+v"(g1[3]), "+v"(g1[4]), "+v"(g1[5]), "+v"(g1[6]),
-                 "+v"(g1[7])
-               :
-               : "memory");
 }
 
 // Cache rows that a tile holds but the softmax masks (tile tails, -1 and
@@ -256,85 +210,87 @@ __device__ inline i16x8 fp8x8_dequant_bf16(uint2 v, float s) {
 }
 
 // ---------------------------------------------------------------------------
-// Attention kernel
+// Attention kernel, dims-split form (native bf16 / fp16 rows)
 // ---------------------------------------------------------------------------
-// Waves: NHG head groups of 32 heads x 4 quarters = 4*NHG waves (two per SIMD
-// for NHG = 2). Wave w -> head group hg = w % NHG, quarter q = w / NHG.
-//   Q·Kᵀ: wave q computes a partial Sᵀ[32 rows x 32 heads] over dims quarter q
-//         (main dims 128q..128q+127 and, for d_qk 576, rope dims 512+16q..+15).
-//   reduce-scatter: the partials of a head group are summed through LDS; wave q
-//         owns the 8 rows {8q + 4*hl + 0..3} (hl = lane / 32) of the sum.
-//   softmax: on the 4 rows x 1 head a lane owns; P (rounded to the input type)
-//         is shared through LDS, so every wave of the head group sees all 32
-//         rows of P. Running max m is shared by the four waves; each keeps a
-//         partial row sum (fp32 P) that is combined once per item.
-//   P·V:  wave q accumulates Oᵀ[dv quarter q (128) x 32 heads] over all rows.
-// Per tile: barrier A (partials written; the oldest stage is free for the
-// next DMA) and barrier B (P written). A rescale (some head's max grew by more
-// than 2^8) is decided workgroup-wide after B and costs one more barrier.
-// fp8 rows (KVF = SAS_KV_FP8_DS_MLA): the main dims are loaded into VGPRs,
-// dequantized to bf16 and written to the same LDS layout, so every read of a
-// stage is the same as for a bf16 cache. Tile it + 2 is converted while tile
-// it's P·V runs, and tile it + 3's loads are issued right after.
+// Waves: NHG head groups of 32 heads x 2 halves of d_qk / d_v = 2*NHG waves,
+// one per SIMD. Wave w -> head group hg = w % NHG, half dh = w / NHG; its
+// partner (same heads, other half) is w ^ NHG.
+//   Q·Kᵀ: partial Sᵀ[32 rows x 32 heads] over dims half dh (main dims
+//         256dh..256dh+255 and, for d_qk 576, rope dims 512+32dh..+31), with
+//         v_mfma_f32_32x32x16 (A = K rows from LDS, B = Qᵀ in VGPRs);
+//   exchange: the two partials of a head group meet through LDS; each wave
+//         adds the other's to its own (fp32 addition is commutative, so both
+//         hold the identical Sᵀ and take identical softmax decisions);
+//   softmax: 16 rows x 1 head per lane, exp2 domain. A head's running max
+//         moves at every tile whose max exceeds it (golden.py:187-191's rule
+//         at 32-row tiles), so the largest score seen so far has P = 1 exactly
+//         when P is rounded to the input type (golden.py:192-196);
+//   P·V:  Oᵀ[dv half dh (256) x 32 heads] += Vᵀ·Pᵀ. Pᵀ is taken straight from
+//         the Sᵀ registers: the accumulator holds rows 8(i/4) + 4(lane/32) +
+//         i%4 in element i, which is the B-operand order of the Vᵀ reads
+//         (k-step kq = elements 8kq..8kq+7).
+// Per tile: barrier 1 (partials written) and barrier 2 (the stage is free and
+// the next tile has landed). Ring of 3 stages: tile t + 2 is issued at the
+// head of iteration t into the stage barrier 2 of iteration t - 1 released,
+// and waited for at the end of iteration t + 1 (two iterations in flight).
+// fp8 rows (KVF = SAS_KV_FP8_DS_MLA): tile t + 2 is loaded into VGPRs at the
+// head of iteration t and dequantized into its stage (the same bf16 layout)
+// before barrier 2 of iteration t, so every read of a stage is the bf16 one.
 template <int DQK, int DV, int NHG, typename T, int KVF>
-__global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
-  constexpr int NQ = 4;                  // dims / dv quarters per head group
-  constexpr int NW = NQ * NHG;           // waves per workgroup
+__global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
+  constexpr int NW = 2 * NHG;            // waves per workgroup
   constexpr int MB = 32 * NHG;           // heads per item (m-block)
   constexpr int NT = 64 * NW;            // threads
   constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
   constexpr bool FP8 = KVF == SAS_KV_FP8_DS_MLA;
   constexpr int ROWB = FP8 ? SAS_FP8_ROW_BYTES : DQK * 2;  // bytes per cache row in HBM
   constexpr int ROPE_OFF = FP8 ? 528 : 1024;               // byte offset of the rope dims
-  constexpr int NKS_MAIN = 8;            // k-steps over 128 main dims
-  constexpr int NKS = NKS_MAIN + (ROPE ? 1 : 0);
-  constexpr int DVB = DV / 32 / NQ;      // 32-wide dv blocks per wave (4)
+  constexpr int NKS_MAIN = 16;           // k-steps over the 256 main dims of a half
+  constexpr int NKS = NKS_MAIN + (ROPE ? 2 : 0);
+  constexpr int DVB = DV / 2 / 32;       // 32-wide dv blocks per wave (8)
+  constexpr int NSTG = 3;                // LDS ring depth
   constexpr int STAGE_BYTES = MAIN_BYTES + (ROPE ? ROPE_BYTES : 0);
-  constexpr int ROWS_PER_WAVE = TILE / NW;            // main-part DMA instructions per wave
-  constexpr int NROPE = ROPE ? TILE / 8 : 0;          // rope DMA instructions per tile
-  constexpr int PSTRIDE = 80;            // bytes per head in the P buffer (64 + pad)
+  constexpr int ROWS_PER_WAVE = TILE / NW;             // main-part DMA instructions per wave
+  constexpr int NROPE = ROPE ? TILE / 8 : 0;           // rope DMA instructions per tile
+  constexpr int ROPE_PER_WAVE = NROPE / NW;            // 1 or 2 (0 for d_qk 512)
+  constexpr int DMA_PER_TILE = ROWS_PER_WAVE + ROPE_PER_WAVE;  // this wave's per tile
+  constexpr int RCH = 4 * NT;            // positions resolved into LDS at a time
   static_assert(DQK == 512 || DQK == 576, "head_dim");
   static_assert(DV == 512, "head_dim_v");
   static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
-  static_assert(TILE % NW == 0, "rows per wave");
-  static_assert(DVB == 4, "two groups of four dv blocks per wave");
-  static_assert(NROPE <= NW, "at most one rope DMA instruction per wave");
+  static_assert(TILE % NW == 0 && NROPE % NW == 0, "DMA split");
+  static_assert(DMA_PER_TILE <= 63, "vmcnt range");
   static_assert(!FP8 || (ROPE && __is_same(T, __bf16)), "fp8 rows: head_dim 576, bf16");
-  constexpr int RPL = 2 * ROWS_PER_WAVE;  // fp8 path: rope bytes per lane per tile (8 or 16)
+  constexpr int RPL = 2 * ROWS_PER_WAVE;  // fp8 rows: rope bytes per lane per tile (16 or 32)
   typedef uint32_t ropev __attribute__((ext_vector_type(RPL / 4)));
   typedef MfmaOps<T> Ops;
 
-  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTAGE * STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) f32x4 xpart[NHG][NQ][NQ][64];  // partial Sᵀ [dest][src]
-  __shared__ __attribute__((aligned(16))) unsigned char pbuf[NHG][32 * PSTRIDE];
-  __shared__ float mbuf[NHG][NQ][32];   // per-quarter row max (also the l combine)
-  __shared__ __attribute__((aligned(8))) unsigned char flags[8];  // per-wave rescale votes
-  __shared__ uint32_t rowid[RCHUNK];
-  __shared__ uint32_t tmask[RCHUNK / TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTG * STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) f32x4 xbuf[NW][4][64];  // partial Sᵀ of each wave
+  __shared__ uint32_t rowid[RCH];
+  __shared__ uint32_t tmask[RCH / TILE];
   __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hg = w % NHG;
-  const int q = w / NHG;
+  const int dh = w / NHG;
+  const int partner = w ^ NHG;
   const int hlocal = hg * 32 + (lane & 31);  // head within the item's m-block
   const int hblocks = (a.num_heads + MB - 1) / MB;
   const int hl = lane >> 5;
-  // Kᵀ operand: row lane%32, main chunk 16q + 2ks + hl, rope chunk 64 + 2q + hl
+  // Kᵀ operand: row lane%32, main chunk 32dh + 2ks + hl (dims 256dh + 16ks + 8hl),
+  // rope chunk 4dh + 2(ks - 16) + hl
   const int r_qk = lane & 31;
-  const int qk_base = main_row_base(r_qk) + (16 * q + hl) * 16;
-  const int rope_off = MAIN_BYTES + rope_slot(r_qk, 2 * q + hl) * 16;
+  const int qk_base = main_row_base(r_qk) + (32 * dh + hl) * 16;
+  const int rope_off0 = MAIN_BYTES + rope_slot(r_qk, 4 * dh + hl) * 16;
+  const int rope_off1 = MAIN_BYTES + rope_slot(r_qk, 4 * dh + 2 + hl) * 16;
   // Vᵀ operand (ds_read_b64_tr_b16): 16-lane group (lane>>4) reads rows
-  // 4*hl + (lane&15)/4 (+16k, +8) at dv 128q + 16*((lane>>4)&1) + 4*(lane&3) (+32d).
+  // 4*hl + (lane&15)/4 (+16kq, +8) at dv 256dh + 16*((lane>>4)&1) + 4*(lane&3) (+32d).
   // Row r+16 has the same rotation as r; row r+8 (r%8 < 4) has rotation +2.
-  const int tr_base = main_row_base(4 * hl + ((lane & 15) >> 2)) + q * (DV / NQ) * 2 +
+  const int tr_base = main_row_base(4 * hl + ((lane & 15) >> 2)) + dh * DV +
                       ((lane >> 4) & 1) * 32 + (lane & 3) * 8;
-  // P buffer: per head 32 bf16 in k-operand order. Position 16k + 8h + i holds
-  // row 16k + 4h + i (i < 4) or 16k + 8 + 4h + (i - 4), matching the Vᵀ reads.
-  // Wave q's rows 8q + 4hl + jj sit at 16(q/2) + 8hl + 4(q%2) + jj.
-  unsigned char* prow = &pbuf[hg][(lane & 31) * PSTRIDE];
-  const int pwr_off = (16 * (q >> 1) + 8 * hl + 4 * (q & 1)) * 2;
 
   int s2b = a.s2_base;
   int nfa = a.num_fa;
@@ -361,24 +317,18 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
   const char* ori_kv = (const char*)a.ori_kv;
   const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
   const float sc = a.softmax_scale * LOG2E;
-  if (tid < 8) flags[tid] = 0;  // bytes of absent waves stay 0
   if (tid < 2) first_neg[tid] = INT32_MAX;
   __syncthreads();
 
-  // Sinks of this lane's head in the (at most two: num_heads <= 128, 64-head
-  // items above 32 heads) head blocks of an item, loaded once: a load per
-  // item would also wait for the previous item's output stores (one in-order
-  // counter covers loads and stores). The wait the compiler can see keeps
-  // it from re-waiting at every use inside the item loop.
+  // Sinks of this lane's head in the (at most two) head blocks of an item,
+  // loaded once: a load per item would also wait for the previous item's output
+  // stores (one in-order counter covers loads and stores).
   const float sink_hb0 = hlocal < a.num_heads ? a.sinks[hlocal] : -INFINITY;
   const float sink_hb1 = MB + hlocal < a.num_heads ? a.sinks[MB + hlocal] : -INFINITY;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
   int item_par = 0;  // which first_neg slot the next top-k scan uses
   bool first_item = true;
   for (;;) {
-    // the cursor is uniform: keep it in SGPRs so the per-item length and
-    // prefix reads are scalar loads (a vector load here would wait for the
-    // previous item's output stores, which share its in-order counter)
     b = __builtin_amdgcn_readfirstlane(b);
     m = __builtin_amdgcn_readfirstlane(m);
     // normalise the cursor: skip batches with no (more) query rows
@@ -408,15 +358,15 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
     const int p_hi = bhi * s2b < L ? bhi * s2b : L;
     const bool tok_ok = tok >= 0 && tok < a.total_tokens;
 
-    // query fragment for this wave's dims (B operand of Sᵀ = K·Qᵀ)
+    // query fragment for this wave's dims half (B operand of Sᵀ = K·Qᵀ)
     i16x8 qf[NKS];
-    // ---- online-softmax state: m shared by the head group, l partial per wave ----
-    // (golden.py:156-160 seeds m = sink, l = 1: the 1 goes to one lane of quarter 0;
-    // the row sums of lanes l and l ^ 32 (same head) are added at the end)
+    // ---- online-softmax state (golden.py:156-160 seeds m = sink, l = 1; the 1
+    // goes to the lanes of the lower row half, whose row sums are added to the
+    // upper half's at the end) ----
     const int hb = m - s * hblocks;
     const float sink_v = hb == 0 ? sink_hb0 : sink_hb1;
     float m_run = partial ? -INFINITY : (head_ok ? sink_v * LOG2E : -INFINITY);
-    float l_part = (partial || q != 0 || hl != 0) ? 0.0f : 1.0f;
+    float l_part = (partial || hl != 0) ? 0.0f : 1.0f;
     f32x16 acc[DVB];
 #pragma unroll
     for (int d = 0; d < DVB; ++d)
@@ -437,33 +387,36 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
     bool stop_pending = jmax > 0;
     int cmp_stop = g.n_cmp;
 
-    for (int c0 = p_lo; c0 < p_hi; c0 += RCHUNK) {
-      const int clen = (p_hi - c0) < RCHUNK ? (p_hi - c0) : RCHUNK;
+    for (int c0 = p_lo; c0 < p_hi; c0 += RCH) {
+      const int clen = (p_hi - c0) < RCH ? (p_hi - c0) : RCH;
       const int ntile = (clen + TILE - 1) / TILE;
+      // query fragment of the item (first chunk): compiler-visible loads issued
+      // before the resolution's loads, so they land during its memory round
+      // trips; the compiler's wait for the table words below covers them
+      if (c0 == p_lo) {
+        const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
+                                                 (head_ok ? head : 0)) * DQK;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const int dim = ks < NKS_MAIN ? (256 * dh + 16 * ks + 8 * hl)
+                                        : (512 + 32 * dh + 16 * (ks - NKS_MAIN) + 8 * hl);
+          i16x8 v = *(const i16x8*)(qrow + dim);
+          qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        }
+      }
       // ---- resolve positions -> cache rows (bit 31: compressed cache) ----
-      // Thread tid owns positions c0 + e*NT + tid. Phase 1 issues the top-k
-      // loads, phase 2 the block-table loads, phase 3 packs and publishes.
-      constexpr int PER = RCHUNK / NT;
+      constexpr int PER = RCH / NT;
+      static_assert(PER == 4, "resolution positions per thread");
       int cid[PER];
-      int tab[PER];  // block-table word to read, or -1
-      // Loads are unconditional with clamped, always in-bounds indices (so all
-      // of a phase's loads are in flight together); results are masked after.
-      // (two branches: a load-free path must not inherit the top-k path's wait,
-      // which would also wait for the previous item's output stores)
-      // The -1 scan of the top-k slots [0, jmax) outside this chunk's own
-      // [own_lo, own_hi) (first chunk of a scanned item only): its first
-      // NT * SCAN_PER slots are loaded together with the chunk's own ids.
+      int tab[PER];
       const int own_lo = max(c0 - g.n_win, 0);
       const int own_hi = min(max(c0 + clen - g.n_win, own_lo), jmax);
       const int n_extra = stop_pending ? jmax - (own_hi - own_lo) : 0;
       constexpr int SCAN_PER = 4;
-      auto extra_slot = [&](int x) {  // x-th slot outside the own range
-        return x < own_lo ? x : x + (own_hi - own_lo);
-      };
+      auto extra_slot = [&](int x) { return x < own_lo ? x : x + (own_hi - own_lo); };
       int sv0[SCAN_PER];
       if (scan3) {
-        // all loads issued, then one wait (as asm: the compiler gives such loads
-        // one destination register and a wait each)
+        // all loads issued, then one wait that also ties their destinations
         int v[PER];
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
@@ -478,20 +431,11 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
           const int32_t* src = idx_row + (n_extra > 0 ? extra_slot(xc) : 0);
           asm volatile("global_load_dword %0, %1, off" : "=v"(sv0[e]) : "v"(src) : "memory");
         }
-        static_assert(PER == 2 || PER == 4, "resolution positions per thread");
-        static_assert(SCAN_PER == 4, "scan loads tied below");
-        if constexpr (PER == 2)
-          asm volatile("s_waitcnt vmcnt(0)"
-                       : "+v"(v[0]), "+v"(v[1]), "+v"(sv0[0]), "+v"(sv0[1]), "+v"(sv0[2]),
-                         "+v"(sv0[3])
-                       :
-                       : "memory");
-        else
-          asm volatile("s_waitcnt vmcnt(0)"
-                       : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(sv0[0]),
-                         "+v"(sv0[1]), "+v"(sv0[2]), "+v"(sv0[3])
-                       :
-                       : "memory");
+        asm volatile("s_waitcnt vmcnt(0)"
+                     : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(sv0[0]),
+                       "+v"(sv0[1]), "+v"(sv0[2]), "+v"(sv0[3])
+                     :
+                     : "memory");
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
           const int r = e * NT + tid;
@@ -533,55 +477,23 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         }
         if (mine < g.n_cmp) atomicMin(&first_neg[item_par], mine);
       }
-      // Block-table words (the query fragment is loaded after the resolution).
-      // d_qk 512: as asm loads with one wait, the wait and the tie of their
-      // destination registers being one statement (no copy of a register can be
-      // placed between an asm load and its wait); every load has an in-bounds
-      // address (masked lanes read word 0 of the window table).
-      const bool load_q = c0 == p_lo;
-      if constexpr (!ROPE) {
-        bool tab_ok[PER];
-        int tword[PER];
+      // block-table words (compiler-visible loads with in-bounds addresses)
 #pragma unroll
-        for (int e = 0; e < PER; ++e) {
-          const int r = e * NT + tid;
-          const int pos = c0 + r;
-          const bool win = pos < g.n_win;
-          const int key = win ? g.win_lo + pos : cid[e];
-          const int bsz = win ? a.ori_block_size : a.cmp_block_size;
-          const int tlen = win ? a.ori_table_len : a.cmp_table_len;
-          const int32_t* tbl = win ? a.ori_block_table : a.cmp_block_table;
-          const int bi = key >= 0 ? key / bsz : 0;
-          tab_ok[e] = r < clen && tok_ok && key >= 0 && bi < tlen && (win || cid[e] < g.thr) &&
-                      tbl != nullptr;
-          const int32_t* src = tab_ok[e] ? tbl + (size_t)b * tlen + bi : a.ori_block_table;
-          asm volatile("global_load_dword %0, %1, off" : "=v"(tword[e]) : "v"(src) : "memory");
-        }
-        static_assert(PER == 2 || PER == 4, "resolution positions per thread");
-        if constexpr (PER == 2)
-          asm volatile("s_waitcnt vmcnt(0)" : "+v"(tword[0]), "+v"(tword[1]) : : "memory");
-        else
-          asm volatile("s_waitcnt vmcnt(0)"
-                       : "+v"(tword[0]), "+v"(tword[1]), "+v"(tword[2]), "+v"(tword[3])
-                       : : "memory");
-#pragma unroll
-        for (int e = 0; e < PER; ++e) tab[e] = tab_ok[e] ? tword[e] : -1;
-      } else {
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-          const int r = e * NT + tid;
-          const int pos = c0 + r;
-          const bool win = pos < g.n_win;
-          const int key = win ? g.win_lo + pos : cid[e];
-          const int bsz = win ? a.ori_block_size : a.cmp_block_size;
-          const int tlen = win ? a.ori_table_len : a.cmp_table_len;
-          const int32_t* tbl = win ? a.ori_block_table : a.cmp_block_table;
-          const int bi = key >= 0 ? key / bsz : 0;
-          const bool ok = r < clen && tok_ok && key >= 0 && bi < tlen && (win || cid[e] < g.thr);
-          const int t = (tbl != nullptr) ? tbl[(size_t)b * tlen + (bi < tlen ? bi : tlen - 1)] : -1;
-          tab[e] = ok ? t : -1;
-        }
+      for (int e = 0; e < PER; ++e) {
+        const int r = e * NT + tid;
+        const int pos = c0 + r;
+        const bool win = pos < g.n_win;
+        const int key = win ? g.win_lo + pos : cid[e];
+        const int bsz = win ? a.ori_block_size : a.cmp_block_size;
+        const int tlen = win ? a.ori_table_len : a.cmp_table_len;
+        const int32_t* tbl = win ? a.ori_block_table : a.cmp_block_table;
+        const int bi = key >= 0 ? key / bsz : 0;
+        const bool ok = r < clen && tok_ok && key >= 0 && bi < tlen && (win || cid[e] < g.thr);
+        const int t = (tbl != nullptr) ? tbl[(size_t)b * tlen + (bi < tlen ? bi : tlen - 1)] : -1;
+        tab[e] = ok ? t : -1;
       }
+      // every load so far (table words, query fragment) has landed, as the compiler sees it
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
       if (stop_pending) {
         __syncthreads();  // every thread's atomicMin is in
         cmp_stop = min(first_neg[item_par], g.n_cmp);
@@ -614,46 +526,57 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
 
       // ---- DMA issue for one tile into one ring stage ----
       // main part: wave w fills rows w, w + NW, ...; one 1 KB row per instruction
-      // rope part: instruction i fills rows 8i..8i+7 (8 lanes per row)
-      // branch-free row address (bit 31 of the id selects the compressed cache)
+      // rope part: instruction i (wave i % NW) fills rows 8i..8i+7 (8 lanes per row)
       auto row_ptr = [&](uint32_t id) -> const char* {
         const char* base = (id & 0x80000000u) ? cmp_kv : ori_kv;
         const char* p = base + (size_t)(id & 0x7FFFFFFFu) * ROWB;
         return id == ROW_INVALID ? (const char*)g_zero_row : p;
       };
-      // row addresses a wave needs to issue one tile, computed per lane ahead of
-      // use (off the path between barrier A and the DMA issue): lane j <
-      // ROWS_PER_WAVE holds the address of its j-th main row; for the rope
-      // instruction (waves w < NROPE) lane l holds that of row 8w + l/8.
-      auto main_ptrs = [&](int tile) -> uint64_t {
-        return (uint64_t)(uintptr_t)row_ptr(
-            rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
-      };
-      // (computed by every wave, without a branch; only waves w < NROPE use it)
-      auto rope_ptr = [&](int tile) -> uint64_t {
-        const int wr = ROPE && w < NROPE ? w : 0;
-        return (uint64_t)(uintptr_t)row_ptr(rowid[tile * TILE + 8 * wr + (lane >> 3)]);
-      };
-      // address of main row j from lane j (two v_readlane, no scalar arithmetic)
       auto lane_row = [&](uint64_t ptrs, int j) -> const char* {
         const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ptrs, j);
         const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(ptrs >> 32), j);
         return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
       };
-      auto issue = [&](int stage, uint64_t my_ptrs, uint64_t rope_row) {
-        const uint32_t sbase = kv_base + stage * STAGE_BYTES;
+      // The DMAs of one tile, as DMA_PER_TILE instructions per wave: the row
+      // addresses are gathered first (dma_addrs), then instruction j goes out
+      // with dma_one(j), so the instructions can be spread between MFMAs (a wave
+      // that issues many back to back stalls on the memory pipeline).
+      struct DmaAddrs {
+        uint64_t main;                      // lane j < ROWS_PER_WAVE: this wave's j-th main row
+        const char* rope[ROPE ? ROPE_PER_WAVE : 1];  // per lane: its 16-byte rope piece
+        uint32_t sbase;
+      };
+      auto dma_addrs = [&](int tile) -> DmaAddrs {
+        DmaAddrs d;
+        d.sbase = kv_base + (tile % NSTG) * STAGE_BYTES;
+        d.main = (uint64_t)(uintptr_t)row_ptr(
+            rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
+        if constexpr (ROPE) {
 #pragma unroll
-        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
-          const int r = w + NW * j;
-          dma16_sbase(lane_row(my_ptrs, j), (uint32_t)lane * 16u, sbase + main_row_base(r));
+          for (int k = 0; k < ROPE_PER_WAVE; ++k) {
+            const int i = w + NW * k;  // rope instruction: rows 8i..8i+7
+            const int r = 8 * i + (lane >> 3);
+            const int cr = ((lane & 7) - (r >> 1)) & 7;
+            d.rope[k] = row_ptr(rowid[tile * TILE + r]) + 1024 + cr * 16;
+          }
         }
-        if (ROPE && w < NROPE) {
-          const int r = 8 * w + (lane >> 3);
-          const int cr = ((lane & 7) - (r >> 1)) & 7;
-          const char* src = (const char*)(uintptr_t)rope_row + 1024 + cr * 16;
-          dma16_vaddr(src, sbase + MAIN_BYTES + w * 1024);
+        return d;
+      };
+      auto dma_one = [&](const DmaAddrs& d, int j) {
+        if (j < ROWS_PER_WAVE) {
+          const int r = w + NW * j;
+          dma16_sbase(lane_row(d.main, j), (uint32_t)lane * 16u, d.sbase + main_row_base(r));
+        } else if constexpr (ROPE) {
+          const int k = j - ROWS_PER_WAVE;
+          dma16_vaddr(d.rope[k], d.sbase + MAIN_BYTES + (w + NW * k) * 1024);
         }
       };
+      auto issue = [&](int tile) {
+        const DmaAddrs d = dma_addrs(tile);
+#pragma unroll
+        for (int j = 0; j < DMA_PER_TILE; ++j) dma_one(d, j);
+      };
+
       // ---- fp8 rows: VGPR loads, then dequantize into one ring stage ----
       // wave w takes rows w + NW j (j < ROWS_PER_WAVE): lane l loads bytes 8l..8l+7
       // (dims 8l..8l+7, scale l / 16) of each, and RPL rope bytes of row
@@ -664,10 +587,10 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         ropev rope;
       };
       constexpr int ROPE_LPR = 128 / RPL;  // lanes per row for the rope bytes
-      // (global, non-temporal loads: the rows stream through once, as the
-      // native rows' DMAs do)
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      auto fp8_load = [&](Fp8Tile& f, uint64_t my_ptrs) {
+      auto fp8_load = [&](Fp8Tile& f, int tile) {
+        const uint64_t my_ptrs = (uint64_t)(uintptr_t)row_ptr(
+            rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
         const char* rp = nullptr;
 #pragma unroll
         for (int j = 0; j < ROWS_PER_WAVE; ++j) {
@@ -680,325 +603,223 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
         f.rope = __builtin_nontemporal_load(
             (const SAS_GLOBAL ropev*)(rp + ROPE_OFF + (lane % ROPE_LPR) * RPL));
       };
-      auto fp8_store = [&](const Fp8Tile& f, int stage) {
-        unsigned char* sb = kv_lds + stage * STAGE_BYTES;
+      auto fp8_store = [&](const Fp8Tile& f, int tile) {
+        unsigned char* sb = kv_lds + (tile % NSTG) * STAGE_BYTES;
 #pragma unroll
         for (int j = 0; j < ROWS_PER_WAVE; ++j) {
           const int r = w + NW * j;
           *(i16x8*)(sb + main_row_base(r) + 16 * lane) = fp8x8_dequant_bf16(f.v[j], f.s[j]);
         }
+        // the lane's RPL rope bytes are whole 16-byte chunks; consecutive chunks of a
+        // row need not be adjacent in the rotated rope layout, so one store each
+        static_assert(RPL % 16 == 0, "rope bytes per lane");
         const int r = w + NW * (lane / ROPE_LPR);
-        const int byte = (lane % ROPE_LPR) * RPL;
-        *(ropev*)(sb + MAIN_BYTES + rope_slot(r, byte >> 4) * 16 + (byte & 15)) = f.rope;
+        const int c0r = (lane % ROPE_LPR) * (RPL / 16);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int k = 0; k < RPL / 16; ++k)
+          *(u32x4*)(sb + MAIN_BYTES + rope_slot(r, c0r + k) * 16) =
+              (u32x4){f.rope[4 * k], f.rope[4 * k + 1], f.rope[4 * k + 2], f.rope[4 * k + 3]};
       };
       Fp8Tile fpt;
 
-
       if constexpr (FP8) {
         Fp8Tile f1;
-        fp8_load(fpt, main_ptrs(0));
-        if (ntile > 1) fp8_load(f1, main_ptrs(1));
+        fp8_load(fpt, 0);
+        if (ntile > 1) fp8_load(f1, 1);
         fp8_store(fpt, 0);
         if (ntile > 1) fp8_store(f1, 1);
       } else {
-        issue(0, main_ptrs(0), rope_ptr(0));
-        if (ntile > 1) issue(1, main_ptrs(1), rope_ptr(1));
+        issue(0);
+        if (ntile > 1) issue(1);
       }
-      // query fragment (compiler-visible loads, in flight with tiles 0 and 1)
-      if (load_q) {
-        const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
-                                                 (head_ok ? head : 0)) * DQK;
+      // tile 0 has landed (tile 1's DMAs may be in flight; the query fragment and
+      // the table words were waited for during the resolution)
+      if constexpr (!FP8) {
+        if (ntile > 1) wait_vmcnt<DMA_PER_TILE>(); else wait_vmcnt<0>();
+      }
+      // the query fragment lives in AGPRs (the MFMAs read B operands from them
+      // directly), leaving the VGPRs to the accumulators and prefetch buffers
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const int dim = ks < NKS_MAIN ? (128 * q + 16 * ks + 8 * hl) : (512 + 16 * q + 8 * hl);
-          i16x8 v = *(const i16x8*)(qrow + dim);
-          qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
-        }
-      }
-      // A wait the compiler can see: it clears its pending-load state here, so it
-      // puts no vmcnt wait for qf inside the tile loop (that wait would also drain
-      // the row DMAs in flight on every tile). Also lands tiles 0 and 1.
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
-      if (FP8 && ntile > 2) fp8_load(fpt, main_ptrs(2));
+      for (int ks = 0; ks < NKS; ++ks) asm volatile("" : "+a"(qf[ks]));
       __syncthreads();
 
-      // ---- Sᵀ partial of one tile over this wave's dims quarter (K operands 3 deep) ----
-      auto qk = [&](int stg) -> f32x16 {
-        const unsigned char* kb = kv_lds + stg * STAGE_BYTES;
-        auto kaddr = [&](int ks) -> const i16x8* {
-          return (const i16x8*)(ks < NKS_MAIN ? kb + qk_base + ks * 32 : kb + rope_off);
-        };
-        f32x16 r;
+      // Addresses of the DMAs of tile t (t >= 2), gathered one iteration ahead.
+      // Branch-free past the chunk's last tile: those instructions read the zero
+      // row into the stage they would fill, which nothing reads before the chunk ends.
+      auto next_addrs = [&](int tile) -> DmaAddrs {
+        const bool real = tile < ntile;
+        DmaAddrs d = dma_addrs(real ? tile : 0);
+        d.sbase = kv_base + (tile % NSTG) * STAGE_BYTES;
+        if (!real) {
+          d.main = (uint64_t)(uintptr_t)g_zero_row;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) r[j] = 0.0f;
-        constexpr int PF = 3;
-        i16x8 kbuf[PF];
-#pragma unroll
-        for (int i = 0; i < PF; ++i) kbuf[i] = *kaddr(i);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const i16x8 kop = kbuf[ks % PF];
-          if (ks + PF < NKS) kbuf[ks % PF] = *kaddr(ks + PF);
-          r = Ops::mma(kop, qf[ks], r);
+          for (int k = 0; k < (ROPE ? ROPE_PER_WAVE : 1); ++k) d.rope[k] = (const char*)g_zero_row;
         }
-        return r;
+        return d;
       };
-      // ---- reduce-scatter of the partials: quarter G's rows go to wave G ----
-      auto write_partials = [&](const f32x16& r) {
-#pragma unroll
-        for (int G = 0; G < NQ; ++G)
-          xpart[hg][G][q][lane] = (f32x4){r[4 * G], r[4 * G + 1], r[4 * G + 2], r[4 * G + 3]};
-      };
-
-      // Software pipeline over tiles. Iteration it runs Q·Kᵀ of tile it + 1 (its
-      // MFMAs execute under the softmax of tile it), the softmax and P·V of tile
-      // it, and publishes the partials of tile it + 1:
-      //   barrier A(it): partials of tile it visible; stage (it + 2) % 3 (tile
-      //                  it - 1's) free
-      //   barrier B(it): P of tile it visible
-      // Tile it + 2 is issued at the head of iteration it, into the stage that
-      // barrier A(it) has released (tile it - 1's), and must have landed before
-      // barrier A(it + 1).
-      write_partials(qk(0));
-      __syncthreads();  // barrier A(0)
-      // row addresses of the next tile to issue (tile it + 2 at the head of
-      // iteration it; garbage and unused when there is no such tile)
-      uint64_t pend_main = 0, pend_rope = 0;
-      if constexpr (!FP8) {
-        pend_main = main_ptrs(2);
-        pend_rope = rope_ptr(2);
-      }
-
+      DmaAddrs nd;
+      if constexpr (!FP8) nd = next_addrs(2);
+      typedef const unsigned char SAS_LDS* lds_p;
       for (int it = 0; it < ntile; ++it) {
-        const int stage = it % NSTAGE;
-        const unsigned char* sb = kv_lds + stage * STAGE_BYTES;
-        const bool has_next = it + 1 < ntile;
-        const bool more = it + 2 < ntile;
-        const int nx_tile = it + 3 < ntile ? it + 3 : it;
-        // Vᵀ operands of this tile (the A operand of P·V)
-        const uint32_t trb = (uint32_t)(uintptr_t)(sb + tr_base);
-        i16x4 gbuf[2][8];
-        auto read_vt = [&]() {
-#define SAS_TR_GROUP(GI, DST)                                                              \
-  {                                                                                        \
-    constexpr int q_ = (GI);                                                               \
-    DST[0] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 0 * 64>(trb);                       \
-    DST[1] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 0 * 64>(trb);              \
-    DST[2] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 1 * 64>(trb);                       \
-    DST[3] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 1 * 64>(trb);              \
-    DST[4] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 2 * 64>(trb);                       \
-    DST[5] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 2 * 64>(trb);              \
-    DST[6] = ds_read_tr16<(16 * q_) * MAIN_ROW_BYTES + 3 * 64>(trb);                       \
-    DST[7] = ds_read_tr16<(16 * q_ + 8) * MAIN_ROW_BYTES + 32 + 3 * 64>(trb);              \
-  }
-          SAS_TR_GROUP(0, gbuf[0]);
-          SAS_TR_GROUP(1, gbuf[1]);
-#undef SAS_TR_GROUP
-        };
-        uint32_t vm_tile;
-        uint64_t nx_main, nx_rope = 0;
-        f32x16 st_next;
-        f32x4 sred;
-        if constexpr (!FP8) {
-          // Every LDS read of the Q·Kᵀ / softmax phase is one ordered asm group,
-          // waited for by count: the tile mask and next-DMA row ids, Kᵀ of tile
-          // it + 1 and the partials of tile it; then the Vᵀ operands of tile it,
-          // so they stream in under the Q·Kᵀ MFMAs instead of between barrier B
-          // and P·V. (The fp8 form keeps the reads in source order: the extra
-          // live registers would spill there.)
-          vm_tile = ds_read_b32_asm((uint32_t)(uintptr_t)&tmask[it]);
-          uint32_t rid_main = ds_read_b32_asm((uint32_t)(uintptr_t)&rowid[
-              nx_tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
-          const int wr = ROPE && w < NROPE ? w : 0;
-          uint32_t rid_rope =
-              ds_read_b32_asm((uint32_t)(uintptr_t)&rowid[nx_tile * TILE + 8 * wr + (lane >> 3)]);
-          const unsigned char* kbn = kv_lds + ((it + 1) % NSTAGE) * STAGE_BYTES;
-          const uint32_t ka = (uint32_t)(uintptr_t)(kbn + qk_base);
-          i16x8 kq[NKS];
-          kq[0] = ds_read_b128_asm<0>(ka);
-          kq[1] = ds_read_b128_asm<32>(ka);
-          kq[2] = ds_read_b128_asm<64>(ka);
-          kq[3] = ds_read_b128_asm<96>(ka);
-          kq[4] = ds_read_b128_asm<128>(ka);
-          kq[5] = ds_read_b128_asm<160>(ka);
-          kq[6] = ds_read_b128_asm<192>(ka);
-          kq[7] = ds_read_b128_asm<224>(ka);
-          if constexpr (ROPE) kq[8] = ds_read_b128_asm<0>((uint32_t)(uintptr_t)(kbn + rope_off));
-          const uint32_t xa = (uint32_t)(uintptr_t)&xpart[hg][q][0][lane];
-          i16x8 xp[NQ];
-          xp[0] = ds_read_b128_asm<0>(xa);
-          xp[1] = ds_read_b128_asm<1024>(xa);
-          xp[2] = ds_read_b128_asm<2048>(xa);
-          xp[3] = ds_read_b128_asm<3072>(xa);
-          // Tile it + 2 into the stage tile it - 1 has released (barrier A(it)),
-          // issued behind this phase's first LDS reads so that their latency runs
-          // under the DMA issue's memory-pipeline back-pressure. The LDS DMA
-          // counts in vmcnt only: the lgkmcnt waits below are unchanged.
-          if (it + 2 < ntile) issue((it + 2) % NSTAGE, pend_main, pend_rope);
-          // mask, row ids and Kᵀ have landed (only the four partial reads may be
-          // pending; LDS reads of a wave complete in order). Each asm output
-          // register appears once: a duplicated operand makes the compiler copy
-          // the register before the wait, i.e. before the data has arrived.
-          if constexpr (ROPE)
-            asm volatile("s_waitcnt lgkmcnt(4)"
-                         : "+v"(vm_tile), "+v"(rid_main), "+v"(rid_rope), "+v"(kq[0]), "+v"(kq[1]),
-                           "+v"(kq[2]), "+v"(kq[3]), "+v"(kq[4]), "+v"(kq[5]), "+v"(kq[6]),
-                           "+v"(kq[7]), "+v"(kq[8])
-                         :
-                         : "memory");
-          else
-            asm volatile("s_waitcnt lgkmcnt(4)"
-                         : "+v"(vm_tile), "+v"(rid_main), "+v"(rid_rope), "+v"(kq[0]), "+v"(kq[1]),
-                           "+v"(kq[2]), "+v"(kq[3]), "+v"(kq[4]), "+v"(kq[5]), "+v"(kq[6]),
-                           "+v"(kq[7])
-                         :
-                         : "memory");
-          read_vt();
-          nx_main = (uint64_t)(uintptr_t)row_ptr(rid_main);
-          nx_rope = (uint64_t)(uintptr_t)row_ptr(rid_rope);
-          // ---- Q·Kᵀ of the next tile (results needed only after P·V; on the
-          // last tile it reads a stale stage and is discarded) ----
-#pragma unroll
-          for (int j = 0; j < 16; ++j) st_next[j] = 0.0f;
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) st_next = Ops::mma(kq[ks], qf[ks], st_next);
-          // the partials have landed (at most 15 of the 16 Vᵀ reads pending)
-          asm volatile("s_waitcnt lgkmcnt(15)"
-                       : "+v"(xp[0]), "+v"(xp[1]), "+v"(xp[2]), "+v"(xp[3])
-                       :
-                       : "memory");
-          // fixed summation order over source quarters 0, 1, 2, 3
-          sred = ((__builtin_bit_cast(f32x4, xp[0]) + __builtin_bit_cast(f32x4, xp[1])) +
-                  __builtin_bit_cast(f32x4, xp[2])) + __builtin_bit_cast(f32x4, xp[3]);
-        } else {
-          vm_tile = tmask[it];
-          nx_main = main_ptrs(nx_tile);
-          st_next = qk((it + 1) % NSTAGE);
-          sred = ((xpart[hg][q][0][lane] + xpart[hg][q][1][lane]) + xpart[hg][q][2][lane]) +
-                 xpart[hg][q][3][lane];
+        // stage base as an LDS address, so every read below is one per-lane base
+        // plus an immediate offset
+        const lds_p sb = (lds_p)(kv_base + (uint32_t)((it % NSTG) * STAGE_BYTES));
+        // tile it + 2 into the stage tile it - 1 held (freed by barrier 2 of it - 1):
+        // fp8 rows are loaded here; native rows go out by DMA between the Q·Kᵀ MFMAs
+        // (their addresses were gathered during the previous iteration)
+        if constexpr (FP8) {
+          if (it + 2 < ntile) fp8_load(fpt, it + 2);
         }
 
-        // ---- online softmax (exp2 domain) on rows 8q + 4hl + jj ----
-        const uint32_t vm = vm_tile >> (8 * q + 4 * hl);
-        float sv[4];
+        // ---- partial Sᵀ of this tile over this wave's dims half ----
+        // K operands read KPF k-steps ahead (enough LDS reads in flight for one
+        // wave per SIMD to keep the LDS busy)
+        f32x16 st;
+        {
+          constexpr int KPF = SAS_KPF;
+          const lds_p kb = sb + qk_base;
+          auto kaddr = [&](int ks) -> const i16x8 SAS_LDS* {
+            return (const i16x8 SAS_LDS*)(ks < NKS_MAIN
+                                              ? kb + 32 * ks
+                                              : sb + (ks == NKS_MAIN ? rope_off0 : rope_off1));
+          };
+          i16x8 kbuf[KPF];
+#pragma unroll
+          for (int i = 0; i < KPF; ++i) kbuf[i] = *kaddr(i);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) st[j] = 0.0f;
+          // (scheduling fences keep each read KPF MFMAs ahead of its use; left
+          // alone, the scheduler sinks the reads next to their MFMAs)
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            const i16x8 kop = kbuf[ks % KPF];
+            if (ks + KPF < NKS) kbuf[ks % KPF] = *kaddr(ks + KPF);
+            st = Ops::mma(kop, qf[ks], st);
+            // DMA instruction j of tile it + 2 after MFMA j * NKS / DMA_PER_TILE
+            if constexpr (!FP8) {
+#pragma unroll
+              for (int j = 0; j < DMA_PER_TILE; ++j)
+                if ((j * NKS) / DMA_PER_TILE == ks) dma_one(nd, j);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xbuf[w][j][lane] = (f32x4){st[4 * j], st[4 * j + 1], st[4 * j + 2], st[4 * j + 3]};
+        const uint32_t vm = tmask[it] >> (4 * hl);
+        __syncthreads();  // barrier 1: both partials of every head group are written
+        DmaAddrs nd3;
+        if constexpr (!FP8) nd3 = next_addrs(it + 3);  // (rowid reads under the softmax)
+
+        // ---- full Sᵀ = own + partner's (the same float sums on both waves) ----
+        float sv[16];
+        {
+          f32x4 o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = xbuf[partner][j][lane];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sv[4 * j + e] = st[4 * j + e] + o[j][e];
+        }
+        // ---- online softmax (exp2 domain) on rows 8(i/4) + 4hl + i%4 ----
+        // (masking only on tiles with invalid rows: tile tails, -1 / out-of-range ids)
+        if (__builtin_amdgcn_readfirstlane(tmask[it]) != 0xFFFFFFFFu) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            sv[i] = ((vm >> (8 * (i / 4) + (i % 4))) & 1u) ? sv[i] : -INFINITY;
+        }
         float mloc = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sv[e] = ((vm >> e) & 1u) ? sred[e] * sc : -INFINITY;
-          mloc = fmaxf(mloc, sv[e]);
+        for (int i = 0; i < 16; ++i) {
+          sv[i] = sv[i] * sc;
+          mloc = fmaxf(mloc, sv[i]);
         }
         mloc = wave_max_pair(mloc);
-        // lanes l and l ^ 32 store the same value to the same word (no branch)
-        mbuf[hg][q][lane & 31] = mloc;
-        const bool need_any = __any(mloc > m_run + RESCALE_TAU);
-        flags[w] = need_any ? 1 : 0;
-        float pv[4];
-        auto make_p = [&]() {
-          i16x4 pk4;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            pv[e] = (sv[e] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sv[e] - m_run);
-            pk4[e] = Ops::from_f32(pv[e]);
-          }
-          *(i16x4*)(prow + pwr_off) = pk4;
-        };
-        make_p();
-        // next DMA addresses, computed before barrier B
-        pin_u64(nx_main);
-        if (!FP8) pin_u64(nx_rope);
-        __syncthreads();  // barrier B(it)
-        // fp8 rows: partials of tile it + 1 published here, so the Sᵀ registers are
-        // free during P·V (every wave has read tile it's partials before barrier
-        // B; on the last tile they are garbage and never read)
-        if (FP8) write_partials(st_next);
-
-        // rescale votes and the P operand of both k-steps (and, for fp8 rows,
-        // Vᵀ of the whole tile): issued together, then one wait (none of the
-        // asm outputs is touched before it)
-        const uint32_t pka = (uint32_t)(uintptr_t)(prow + 16 * hl);
-        uint64_t votes = ds_read_b64_asm((uint32_t)(uintptr_t)flags);
+        const bool grow = mloc > m_run;
+        const float m_new = grow ? mloc : m_run;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // -inf -> 0
+        m_run = m_new;
+        l_part *= alpha;
+        // a head with no key and no sink yet (m_run = -inf) has every score -inf:
+        // subtracting 0 instead keeps its P at exactly 0
+        const float m_sub = m_run == -INFINITY ? 0.0f : m_run;
         i16x8 pk[2];
-        pk[0] = ds_read_b128_asm<0>(pka);
-        pk[1] = ds_read_b128_asm<32>(pka);
-        if constexpr (FP8) read_vt();
-        lds_wait_pv(votes, pk, gbuf[0], gbuf[1]);
-        if (__builtin_amdgcn_readfirstlane((uint32_t)(votes | (votes >> 32)))) {
-          // rescale: every wave of the head group derives the same new max
-          float mt = mbuf[hg][0][lane & 31];
 #pragma unroll
-          for (int i = 1; i < NQ; ++i) mt = fmaxf(mt, mbuf[hg][i][lane & 31]);
-          if (mt > m_run + RESCALE_TAU) {
-            const float m2 = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m2);  // m_run = -inf -> 0
-            l_part *= alpha;
-#pragma unroll
-            for (int d = 0; d < DVB; ++d)
-#pragma unroll
-              for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
-            m_run = m2;
-          }
-          make_p();         // rewrite this wave's rows with the new max (the P
-          __syncthreads();  // read above is void and is repeated after barrier C)
-          pk[0] = *(const i16x8*)(prow + 16 * hl);
-          pk[1] = *(const i16x8*)(prow + 32 + 16 * hl);
+        for (int i = 0; i < 16; ++i) {
+          const float p = __builtin_amdgcn_exp2f(sv[i] - m_sub);
+          l_part += p;
+          pk[i / 8][i % 8] = Ops::from_f32(p);
         }
-        l_part += (pv[0] + pv[1]) + (pv[2] + pv[3]);
 
-        // ---- Oᵀ += Vᵀ · Pᵀ over both 16-row k-steps ----
-        // (issue priority to this wave's MFMA chain while its SIMD partner runs
-        // VALU / LDS work)
-        __builtin_amdgcn_s_setprio(1);
+        // ---- Oᵀ = alpha·Oᵀ + Vᵀ·Pᵀ over both 16-row k-steps ----
+        // (Vᵀ operands read VPF MFMAs ahead; MFMA i = dv block i / 2, k-step i % 2.
+        // Multiplying every tile costs less than branching on whether any head's
+        // max moved: the two paths would hold the accumulators in different registers)
+        auto pv_tile = [&](auto rescale) {
+          constexpr int VPF = SAS_VPF;
+          constexpr int NPV = 2 * DVB;
+          const lds_p vb = sb + tr_base;
+          typedef i16x4 SAS_LDS* lds4;
+          auto vop = [&](int i) -> i16x8 {
+            const int d = i >> 1, kq = i & 1;
+            const i16x4 g0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds4)(vb + (16 * kq) * MAIN_ROW_BYTES + d * 64));
+            const i16x4 g1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds4)(vb + (16 * kq + 8) * MAIN_ROW_BYTES + 32 + d * 64));
+            return (i16x8){g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+          };
+          i16x8 vbuf[VPF];
 #pragma unroll
-        for (int kq = 0; kq < 2; ++kq)
+          for (int i = 0; i < VPF; ++i) vbuf[i] = vop(i);
+          // (no scheduling fences here: the compiler's own interleaving of the
+          // rescale multiplies with the MFMAs measured faster than fenced orders)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const i16x4* g = gbuf[kq];
-            const i16x8 aop = {g[2 * e][0],     g[2 * e][1],     g[2 * e][2],     g[2 * e][3],
-                               g[2 * e + 1][0], g[2 * e + 1][1], g[2 * e + 1][2], g[2 * e + 1][3]};
-            acc[e] = Ops::mma(aop, pk[kq], acc[e]);
+          for (int i = 0; i < NPV; ++i) {
+            const int d = i >> 1, kq = i & 1;
+            if constexpr (decltype(rescale)::value) {
+              if (kq == 0) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
+              }
+            }
+            const i16x8 aop = vbuf[i % VPF];
+            if (i + VPF < NPV) vbuf[i % VPF] = vop(i + VPF);
+            acc[d] = Ops::mma(aop, pk[kq], acc[d]);
           }
-        __builtin_amdgcn_s_setprio(0);
-        // fp8 rows: stage (it + 2) % 3 last held tile it - 1, read before barrier A(it)
+        };
+        pv_tile(std::true_type{});
+
         if constexpr (FP8) {
-          if (more) fp8_store(fpt, (it + 2) % NSTAGE);
-          if (it + 3 < ntile) fp8_load(fpt, nx_main);
+          // tile it + 2 into its stage (tile it - 1's, free since barrier 2 of it - 1)
+          if (it + 2 < ntile) fp8_store(fpt, it + 2);
+        } else {
+          // this wave's share of tile it + 1 has landed (tile it + 2's may be in flight)
+          wait_vmcnt<DMA_PER_TILE>();
         }
-        if (has_next) {
-          if (!FP8) write_partials(st_next);
-          if (!FP8) wait_vmcnt<0>();  // this wave's share of tile it + 2 has landed
-          __syncthreads();            // barrier A(it + 1)
-          if constexpr (!FP8) {       // tile it + 3 is issued at the next loop head
-            pend_main = nx_main;
-            pend_rope = nx_rope;
-          }
-        }
+        __syncthreads();  // barrier 2: stage and partials free; tile it + 1 in LDS
+        if constexpr (!FP8) nd = nd3;
       }
-      __syncthreads();  // rowid / tmask / ring are rewritten by the next chunk or item
+      if constexpr (!FP8) wait_vmcnt<0>();  // the last (zero-row) DMAs have landed
     }
 
-    // ---- combine the row sums of the four quarters (fixed order) ----
-    l_part = wave_sum_pair(l_part);
-    if (hl == 0) mbuf[hg][q][lane & 31] = l_part;
-    __syncthreads();
-    const float l_run = ((mbuf[hg][0][lane & 31] + mbuf[hg][1][lane & 31]) +
-                         mbuf[hg][2][lane & 31]) + mbuf[hg][3][lane & 31];
-    __syncthreads();  // mbuf is reused by the next item
+    // ---- row sums of the two row halves (lanes l and l ^ 32, same head) ----
+    const float l_run = wave_sum_pair(l_part);
 
     // ---- epilogue: the item's rows go out through LDS (the ring is free), so
-    // every store instruction writes whole rows (1 KB per wave) instead of
-    // 16- or 32-byte pieces of 32 rows ----
+    // every store instruction writes whole rows ----
     {
       unsigned char* stg = kv_lds;
       const int nh = min(MB, a.num_heads - hb * MB);  // heads of this item
-      // opaque copies of the thread indices: the addresses below are then
-      // computed here, not hoisted out of the item loop (where they would
-      // occupy registers across the tile loop)
-      int tid_e = tid, hl_e = hlocal, dv_e = q * (DV / NQ) + 4 * hl;
+      int tid_e = tid, hl_e = hlocal, dv_e = dh * (DV / 2) + 4 * hl;
       asm volatile("" : "+v"(tid_e), "+v"(hl_e), "+v"(dv_e));
       if (!partial) {
         constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes)
         constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
-        static_assert(MB * SROW <= NSTAGE * STAGE_BYTES, "output staging");
+        static_assert(MB * SROW <= NSTG * STAGE_BYTES, "output staging");
         const float inv = 1.0f / l_run;
 #pragma unroll
         for (int d = 0; d < DVB; ++d)
@@ -1018,22 +839,22 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
             const int h = c / CPR, c16 = c - h * CPR;
             *(i16x8*)(obase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
           }
-          if (q == 0 && hl == 0 && head_ok)
+          if (dh == 0 && hl == 0 && head_ok)
             a.lse[(size_t)tok * a.num_heads + hb * MB + hl_e] = (m_run + __log2f(l_run)) * LN2;
         }
       } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
-        // fp32 partials (acc / l), staged in two halves of the dv range
+        // fp32 partials (acc / l), staged one dv half (= one wave of each pair) at a time
         constexpr int HALF = DV / 2;
         constexpr int SROW = HALF * 4 + 16;
         constexpr int CPR = HALF * 4 / 16;
-        static_assert(MB * SROW <= NSTAGE * STAGE_BYTES, "partial staging");
+        static_assert(MB * SROW <= NSTG * STAGE_BYTES, "partial staging");
         const bool empty = !(l_run > 0.0f);
         const float inv = empty ? 0.0f : 1.0f / l_run;
         char* wbase = (char*)(a.workspace + (size_t)slot * MB * DV);
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           if (half) __syncthreads();  // the first half has been read out
-          if ((q >> 1) == half) {  // waves whose dv quarter lies in this half
+          if (dh == half) {
 #pragma unroll
             for (int d = 0; d < DVB; ++d)
 #pragma unroll
@@ -1052,10 +873,9 @@ __global__ __launch_bounds__(256 * NHG) void attn_kernel(const SasAttnArgs a) {
                 *(const f32x4*)(stg + h * SROW + c16 * 16);
           }
         }
-        if (q == 0 && hl == 0 && head_ok) {
+        if (dh == 0 && hl == 0 && head_ok) {
           float* wl = a.workspace + (size_t)a.num_partial_slots * MB * DV;
-          wl[(size_t)slot * MB + hl_e] =
-              empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
+          wl[(size_t)slot * MB + hl_e] = empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
         }
       }
     }
@@ -1233,8 +1053,8 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   const int phases = a.phases == 0 ? 3 : a.phases;
   if (phases & 1) {
     const int per_xcd = (a.num_fa + 7) / 8;
-    hipLaunchKernelGGL((attn_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd), dim3(256 * NHG),
-                       0, st, a);
+    hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
+                       dim3(128 * NHG), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -7,20 +7,24 @@ rows over up to ~2.5k cached rows, 16-128 heads, a window of 0, 1, 6, 128 or
 top-k width from 1 to 1030 (wider than the compressed prefix, so ``-1``
 padded), cache block sizes of 16 / 64 / 128 and a schedule for 1, 7, 64 or
 256 workgroups (single pieces, multi-chunk items, split items). Inputs follow
-the reference's generators (q, raw KV U(-10, 10); compressed KV U(-5, 10)).
+the reference's generators (q, raw KV U(-10, 10); compressed KV U(-5, 10)):
+peaked attention over values up to 10, where rounding P to bf16 alone moves
+an output by up to ~2e-2.
 
-Asserted for every row: the LSE within 1e-3 relative of golden, and the
-output as accurate as golden against the float64 closed form (max |out -
-exact| <= 2 max |golden - exact| + 2^-9 max |exact|). Reported, not asserted:
-the reference's 99.5 % rule and the per-element 2e-2 bound. With these inputs
-(|V| up to 10, peaked attention) rounding P to bf16 alone moves an output by
-up to ~2e-2, and golden rounds P relative to the running max of 512-row tiles
-while this kernel uses 32-row tiles and a lazily moved max: the two roundings
-differ by up to ~3e-2 in a few elements of a long attended list, and by more
-than 2^-7 relative in ~0.5-1 % of them (those near zero), while both are
-equally far from the exact result. The reference's own cases, where its rule
-is asserted, and the N(0, 1) * 0.5 shapes, where the 2e-2 bound is, are in
-test_gpu_parity.py.
+Asserted for every case (the accuracy contract):
+* against golden, the bound that golden's own algorithm meets when it walks
+  the attended rows in the kernel's 32-row tiles: at least 99.25 % of the
+  elements within the reference's rule (rtol 2^-7, atol 1e-4;
+  test_sparse_attn_sharedkv.py:394-481) and at most one element beyond
+  atol = rtol = 2e-2. Over the 300 configurations of ``oracle.rescale_study``
+  golden at 32-row tiles has at least 99.308 % within the rule (3 cases under
+  the reference's 99.5 %) and no element beyond 2e-2; the kernel's order of
+  rounding (eager running max per 32-row tile) 99.304 % and one element beyond
+  2e-2 in one case. The reference's 99.5 % holds for golden's own 512-row tiles
+  only, so it is reported here, not asserted;
+* the LSE within 1e-3 relative of golden;
+* the output as accurate as golden against the float64 closed form (max
+  |out - exact| <= 2 max |golden - exact| + 2^-9 max |exact|).
 """
 
 import math
@@ -43,6 +47,10 @@ requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
 if HAS_GPU:
     from sparse_attn_sharedkv_amd import sparse_attn_sharedkv, sparse_attn_sharedkv_metadata
 
+# the bound golden's own algorithm meets at the kernel's 32-row tiles (module docstring)
+MIN_PCT_REF_RULE = 99.25
+MAX_BEYOND_2E2 = 1
+
 N_CASES = int(os.environ.get("SAS_SWEEP_CASES", "40"))  # more for a longer validation run
 DTYPE = {"bf16": torch.bfloat16, "fp16": torch.float16}[os.environ.get("SAS_SWEEP_DTYPE", "bf16")]
 
@@ -52,37 +60,7 @@ def _say(msg):
     sys.stdout.flush()
 
 
-def _random_cfg(rng):
-    scenario = int(rng.integers(1, 4))
-    layout = "TND" if rng.random() < 0.6 else "BSND"
-    b = int(rng.integers(1, 5))
-    q_opts = [1, 1, 2, 3, 17, 40]
-    if layout == "TND":
-        qlens = [int(rng.choice(q_opts)) for _ in range(b)]
-    else:
-        qlens = [int(rng.choice(q_opts))] * b
-    kv = [int(q + rng.integers(0, 2500)) for q in qlens]
-    ratio = int(rng.choice([1, 4, 16, 128])) if scenario >= 2 else 4
-    k = int(rng.choice([1, 7, 64, 512, 1030])) if scenario == 3 else 512
-    bs1 = int(rng.choice([16, 64, 128]))
-    bs2 = int(rng.choice([16, 64, 128]))
-    cu = [0]
-    for q in qlens:
-        cu.append(cu[-1] + q)
-    return dict(
-        scenario=scenario, layout_q=layout, B=b, S1=max(qlens),
-        T1=sum(qlens) if layout == "TND" else max(qlens) * b,
-        N1=int(rng.choice([16, 32, 48, 64, 96, 128])), N2=1, D=512, K=k,
-        block_num1=sum(math.ceil(x / bs1) for x in kv) + int(rng.integers(0, 3)),
-        block_num2=sum(max(1, math.ceil((x // ratio) / bs2)) for x in kv) + 1,
-        block_size1=bs1, block_size2=bs2, cu_seqlens_q=cu, seqused_kv=kv,
-        softmax_scale=1.0 / math.sqrt(512), cmp_ratio=ratio,
-        ori_win_left=int(rng.choice([-1, 0, 5, 127, 1023])), ori_win_right=0,
-        ori_mask_mode=4, cmp_mask_mode=3,
-        cores=int(rng.choice([1, 7, 64, 256])))
-
-
-_CASES = [_random_cfg(np.random.default_rng(1000 + i)) for i in range(N_CASES)]
+_CASES = [gen.random_sweep_cfg(np.random.default_rng(1000 + i)) for i in range(N_CASES)]
 
 
 @requires_gpu
@@ -115,6 +93,8 @@ def test_random_configuration(i):
     beyond = int((err > OUT_ATOL + OUT_RTOL * r.abs()).sum())
     _say(f"case {i}: {within:.3f} % within the reference's rtol 2^-7 / atol 1e-4; "
          f"{beyond} elements beyond 2e-2; max |out - golden| {err.max().item():.3g}")
+    assert within >= MIN_PCT_REF_RULE, f"{within:.3f} % within the reference's rule"
+    assert beyond <= MAX_BEYOND_2E2, f"{beyond} elements beyond atol = rtol = 2e-2"
     x, y = lse.cpu(), ref_lse
     fin = torch.isfinite(y)
     assert torch.equal(torch.isfinite(x), fin) and torch.equal(x[~fin], y[~fin]), "lse: non-finite"
