@@ -176,6 +176,18 @@ typedef struct SasAttnArgs {
  * `stream` (a hipStream_t). Asynchronous; no allocation, no host synchronisation. */
 int sas_attention_launch(const SasAttnArgs* args, void* stream);
 
+/* Allocation-free variant of sas_attention_launch (no counterpart in the reference:
+ * for callers that cannot allocate device memory, such as code under HIP graph
+ * capture, tight serving loops and harnesses that forbid allocation). Same arguments
+ * and kernels; args->workspace is ignored and the split-KV partials go to a fixed
+ * per-device scratch array of SAS_NOALLOC_SCRATCH_BYTES inside the library, so
+ * sas_workspace_bytes(num_partial_slots, m_base, head_dim_v) must not exceed it
+ * (else SAS_E_CAPACITY, nothing launched). Calls no hipMalloc/hipFree. All calls on
+ * one device share its scratch array: calls that may overlap on one device (other
+ * streams, concurrent threads) race and must be serialised by the caller. */
+#define SAS_NOALLOC_SCRATCH_BYTES (72ull << 20)
+int sas_attention_launch_noalloc(const SasAttnArgs* args, void* stream);
+
 /* Quantize-on-append into a SAS_KV_FP8_DS_MLA cache (no reference counterpart: the
  * reference has no fp8 cache; this is the producer of the format above).
  * src: [n, 576] bf16 rows (device); slot_mapping: [n] int32 flat row index into the pool

@@ -24,6 +24,10 @@ CFG_OFFSET = SAS_META_SIZE - 8
 META_MAGIC = 0x5A53A355
 
 SAS_OK = 0
+SAS_E_INVALID = -1
+SAS_E_UNSUPPORTED = -2
+SAS_E_CAPACITY = -3
+SAS_E_HIP = -4
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
 KV_NATIVE = 0
@@ -80,8 +84,9 @@ class SasAttnArgs(ctypes.Structure):
 
 
 EXPORTS = ("sas_metadata_build", "sas_metadata_build_device", "sas_workspace_bytes",
-           "sas_attention_launch", "sas_kv_fp8_append", "sas_version", "sas_args_struct_size",
-           "sas_last_error")
+           "sas_attention_launch", "sas_attention_launch_noalloc", "sas_kv_fp8_append",
+           "sas_version", "sas_args_struct_size", "sas_last_error")
+NOALLOC_SCRATCH_BYTES = 72 << 20  # SAS_NOALLOC_SCRATCH_BYTES
 
 _lock = threading.Lock()
 _lib = None
@@ -111,6 +116,8 @@ def load() -> ctypes.CDLL:
         lib.sas_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.sas_attention_launch.restype = ctypes.c_int
         lib.sas_attention_launch.argtypes = [ctypes.POINTER(SasAttnArgs), ctypes.c_void_p]
+        lib.sas_attention_launch_noalloc.restype = ctypes.c_int
+        lib.sas_attention_launch_noalloc.argtypes = [ctypes.POINTER(SasAttnArgs), ctypes.c_void_p]
         lib.sas_kv_fp8_append.restype = ctypes.c_int
         lib.sas_kv_fp8_append.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                           ctypes.c_int, ctypes.c_int64, ctypes.c_void_p]

@@ -39,6 +39,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -1162,6 +1163,68 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     return SAS_E_HIP;
   }
   return SAS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free launch: the split-KV partials go to a fixed device array
+// ---------------------------------------------------------------------------
+namespace sas {
+// One copy per device (the runtime places it when the library's code object is
+// loaded; each device keeps it until the process ends). In host code `scratch`
+// names a host-side stand-in: only the address from hipGetSymbolAddress, taken
+// once per device with that device current, is passed to kernels.
+__device__ __attribute__((aligned(256))) float scratch[SAS_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+constexpr int MAX_DEVICES = 64;
+static float* g_scratch_ptr[MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// Address of this device's scratch array (resolved on the first call per device).
+static int scratch_ptr(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(std::string("sas_attention_launch_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+    return SAS_E_HIP;
+  }
+  if (dev < 0 || dev >= MAX_DEVICES) {
+    set_error("sas_attention_launch_noalloc: device index out of range");
+    return SAS_E_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error(std::string("sas_attention_launch_noalloc: hipGetSymbolAddress: ") +
+                hipGetErrorString(e));
+      return SAS_E_HIP;
+    }
+    g_scratch_ptr[dev] = (float*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SAS_OK;
+}
+}  // namespace sas
+
+extern "C" int sas_attention_launch_noalloc(const SasAttnArgs* a, void* stream) {
+  if (!a) {
+    sas::set_error("sas_attention_launch_noalloc: null args");
+    return SAS_E_INVALID;
+  }
+  const int64_t need = sas_workspace_bytes(a->num_partial_slots, a->m_base, a->head_dim_v);
+  if (need > (int64_t)SAS_NOALLOC_SCRATCH_BYTES) {
+    sas::set_error("sas_attention_launch_noalloc: the schedule's split-KV workspace (" +
+                   std::to_string(need) + " bytes for " + std::to_string(a->num_partial_slots) +
+                   " partial slots) exceeds the fixed scratch of " +
+                   std::to_string((long long)SAS_NOALLOC_SCRATCH_BYTES) + " bytes");
+    return SAS_E_CAPACITY;
+  }
+  float* ws = nullptr;
+  const int rc = sas::scratch_ptr(&ws);
+  if (rc != SAS_OK) return rc;
+  SasAttnArgs b = *a;
+  b.workspace = ws;  // the caller's workspace pointer, if any, is not used
+  return sas_attention_launch(&b, stream);
 }
 
 extern "C" int sas_version(void) { return 110; }

@@ -1,0 +1,71 @@
+"""The allocation-free entry point ``sas_attention_launch_noalloc`` on a GPU.
+
+It runs the same kernels as ``sas_attention_launch`` with the split-KV partials
+in the library's fixed per-device scratch array instead of the caller's
+workspace. Checked through the C-ABI: bitwise-equal outputs to
+``sas_attention_launch`` on two calls in a row (the second on a smaller
+input, so the scratch array holds the first call's partials when it starts),
+for host-built schedules with split items and for a device-built schedule;
+and a schedule whose partials do not fit is refused before any launch.
+"""
+
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from oracle import gen
+
+pytestmark = pytest.mark.gpu
+
+HAS_GPU = torch.cuda.is_available()
+requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
+
+if HAS_GPU:
+    from sparse_attn_sharedkv_amd import _lib, api
+
+
+def _say(msg):
+    print(f"[gpu-noalloc] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _launch(entry, prep):
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    prep.args.phases = 0
+    prep.out.fill_(float("nan"))
+    prep.lse.fill_(float("nan"))
+    rc = getattr(_lib.load(), entry)(ctypes.byref(prep.args), st)
+    assert rc == _lib.SAS_OK, _lib.last_error()
+    torch.cuda.synchronize()
+    return prep.out.clone(), prep.lse.clone()
+
+
+@requires_gpu
+@pytest.mark.parametrize("name,batches,extra", [
+    ("mla_decode_b64_h128_k2048", (8, 2), {"core_num": 256}),      # every item split in two
+    ("swa_topk_decode_b32_h64_k512", (16, 3), {"core_num": 512}),  # items in several pieces
+    ("mla_decode_b64_h128_k2048", (6, 1), {"schedule": "device"}),  # device-built schedule
+])
+def test_noalloc_matches_launch_two_calls(name, batches, extra):
+    for batch in batches:  # the second call is smaller than the first
+        _say(f"{name} batch={batch} {extra}")
+        kw = gen.build_workload(name, device="cuda", seed=40 + batch, batch=batch)
+        prep = api.prepare(**kw, **extra)
+        assert prep.args.num_fd != 0, "the case must exercise the split-KV workspace"
+        o_ref, l_ref = _launch("sas_attention_launch", prep)
+        o, l = _launch("sas_attention_launch_noalloc", prep)
+        assert torch.isfinite(o_ref.float()).all()
+        assert torch.equal(o, o_ref) and torch.equal(l, l_ref)
+
+
+@requires_gpu
+def test_noalloc_refuses_a_workspace_beyond_the_scratch():
+    kw = gen.build_workload("mla_decode_b64_h128_k2048", device="cuda", seed=3, batch=2)
+    prep = api.prepare(**kw, core_num=256)
+    a = _lib.SasAttnArgs.from_buffer_copy(prep.args)
+    a.num_partial_slots = _lib.NOALLOC_SCRATCH_BYTES // (a.m_base * (a.head_dim_v + 1) * 4) + 1
+    rc = _lib.load().sas_attention_launch_noalloc(ctypes.byref(a), None)
+    assert rc == _lib.SAS_E_CAPACITY
+    assert "scratch" in _lib.last_error()
