@@ -165,8 +165,12 @@ typedef struct SasAttnArgs {
    * config row. A config row without SAS_META_MAGIC, or built for another head count,
    * m_base or larger capacities, makes the launch write NaN to out and lse. */
   int32_t num_fa, num_fd, num_partial_slots, s2_base, m_base;
-  /* kernels to enqueue: bit 0 attention, bit 1 split-KV merge; 0 means both.
-   * A caller may enqueue the two phases as separate calls (attention first). */
+  /* kernels to enqueue: bit 0 attention, bit 1 split-KV merge; neither means both.
+   * A caller may enqueue the two phases as separate calls (attention first).
+   * SAS_PHASE_PIPELINED (bit 2) runs native rows through the attention kernel
+   * that fp8 rows use (two waves per SIMD, software-pipelined); by default native
+   * rows take the one-wave-per-SIMD kernel, which is faster on them. Results of the
+   * two kernels agree to within rounding, not bit for bit. */
   int32_t phases;
   /* row format of ori_kv and cmp_kv: SAS_KV_NATIVE or SAS_KV_FP8_DS_MLA */
   int32_t kv_format;
@@ -185,6 +189,7 @@ int sas_attention_launch(const SasAttnArgs* args, void* stream);
  * (else SAS_E_CAPACITY, nothing launched). Calls no hipMalloc/hipFree. All calls on
  * one device share its scratch array: calls that may overlap on one device (other
  * streams, concurrent threads) race and must be serialised by the caller. */
+#define SAS_PHASE_PIPELINED 4
 #define SAS_NOALLOC_SCRATCH_BYTES (72ull << 20)
 int sas_attention_launch_noalloc(const SasAttnArgs* args, void* stream);
 

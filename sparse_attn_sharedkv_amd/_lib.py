@@ -33,6 +33,7 @@ DTYPE_FP16 = 1
 KV_NATIVE = 0
 KV_FP8_DS_MLA = 1
 FP8_ROW_BYTES = 656
+SAS_PHASE_PIPELINED = 4        # SasAttnArgs.phases bit: native rows through the pipelined kernel
 SCHED_DEVICE = -1             # SasAttnArgs.num_fd: schedule summary read on the device
 DEV_SCHED_MAX_BATCH = 4096
 DEV_SCHED_MAX_ITEMS = 16384

@@ -888,6 +888,785 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Attention kernel, software-pipelined form (two waves per SIMD)
+// ---------------------------------------------------------------------------
+// Waves: NHG head groups of 32 heads x 4 = 4*NHG waves (two per SIMD at 64
+// heads). Wave w -> head group hg = w / 4 and quarter wq = w % 4, with row half
+// rh = wq % 2 and head half qh = wq / 2.
+//   Q·Kᵀ:  Sᵀ[16 rows (16rh ..) x 16 heads (hg*32 + 16qh ..)] over the whole
+//          d_qk with v_mfma_f32_16x16x32 (A = the wave's K rows from LDS, B = Qᵀ
+//          in AGPRs), as two chains (even / odd k-steps) added at the end.
+//   softmax: in registers, 4 rows x 1 head per lane; a head's 16 rows of the
+//          wave sit in lanes l, l^16, l^32, l^48 (max / sum over them by
+//          permlane swaps), the tile max over both row halves meets through
+//          LDS. The running max moves at every tile whose max exceeds it
+//          (golden.py:187-191's rule at 32-row tiles); both row halves hold the
+//          same max, factor and running max of a head. Pᵀ (input type) of the
+//          wave's rows and the rescale factors go to LDS.
+//   P·V:   Oᵀ[dv quarter wq (128) x 32 heads of hg] += Vᵀ·Pᵀ with
+//          v_mfma_f32_32x32x16 (A = Vᵀ via ds_read_b64_tr_b16, B = Pᵀ of the
+//          head group from LDS).
+// Pipeline, per tile t (4-stage ring):
+//   phase A: Q·Kᵀ MFMAs of tile t + 1 with the softmax of tile t between them,
+//            and the row DMAs of tile t + 3 (into the stage tile t - 1 left);
+//            then the wave's row max of tile t + 1 per head to LDS;
+//   barrier 1 (Pᵀ and factors of tile t, row maxima of t + 1 written);
+//   phase B: tile max of t + 1; rescale and P·V of tile t; wait for this
+//            wave's DMAs of tile t + 2;
+//   barrier 2 (tile t + 2 in LDS, stage t and the exchange buffers free).
+// Pᵀ of tile t lives in the rope part of stage t (read by Q·Kᵀ of tile t during
+// phase A of t - 1, refilled by the DMAs issued in phase A of t + 1).
+// fp8 rows (KVF = SAS_KV_FP8_DS_MLA): tile t + 2 is loaded into VGPRs in phase A
+// and dequantized into its stage in phase B.
+// LDS stage layout of the pipelined kernel (one 32-row tile). Main part: row r
+// (dims 0..511, 1 KB) at ring_row_base(r): rows permuted within groups of four
+// and offset by 0..3 sixteen-byte slots inside 1088-byte row slots. Rope part
+// (dims 512..575): chunk c of row r at slot 8 r + (c ^ ((r >> 1) & 7)). Both were
+// chosen by measuring SQ_LDS_BANK_CONFLICT on MI355X: the 16x16x32 K-operand
+// reads (16 rows x 4 consecutive chunks per instruction), the transposed Vᵀ reads
+// and the 32x32x16 K-operand reads are all conflict-free in it.
+__device__ __host__ inline int ring_row_base(int r) {
+  const int a = r >> 4, b = (r >> 2) & 3, c = r & 3;
+  return (16 * a + 4 * b + ((c + (b >> 1)) & 3)) * MAIN_ROW_BYTES + 16 * (2 * (b & 1) + a);
+}
+__device__ __host__ inline int ring_rope_slot(int r, int c) { return 8 * r + (c ^ ((r >> 1) & 7)); }
+
+template <int DQK, int DV, int NHG, typename T, int KVF>
+__global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
+  constexpr int NW = 4 * NHG;            // waves per workgroup
+  constexpr int MB = 32 * NHG;           // heads per item (m-block)
+  constexpr int NT = 64 * NW;            // threads
+  constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
+  constexpr bool FP8 = KVF == SAS_KV_FP8_DS_MLA;
+  constexpr int ROWB = FP8 ? SAS_FP8_ROW_BYTES : DQK * 2;  // bytes per cache row in HBM
+  constexpr int ROPE_OFF = FP8 ? 528 : 1024;               // byte offset of the rope dims
+  constexpr int NKS = DQK / 32;          // 16x16x32 k-steps over d_qk (18 or 16)
+  constexpr int NKS_MAIN = 16;           // k-steps over the 512 main dims
+  constexpr int DVQ = DV / 4;            // dv per wave (a quarter)
+  constexpr int DVB = DVQ / 32;          // 32-wide dv blocks per wave (4)
+  constexpr int NSTG = 4;                // LDS ring depth
+  constexpr int STAGE_BYTES = MAIN_BYTES + (ROPE ? ROPE_BYTES : 0);
+  constexpr int PB_HG = 32 * 64;         // Pᵀ of one head group: 32 heads x 32 rows x 2 B
+  constexpr int ROWS_PER_WAVE = TILE / NW;             // main-part DMA instructions per wave
+  constexpr int NROPE = ROPE ? TILE / 8 : 0;           // rope DMA instructions per tile (4)
+  constexpr int DMA_MAX = ROWS_PER_WAVE + (ROPE ? 1 : 0);  // per wave and tile (waves w < NROPE)
+  constexpr int RCH = 1024;              // positions resolved into LDS at a time
+  static_assert(DQK == 512 || DQK == 576, "head_dim");
+  static_assert(DV == 512, "head_dim_v");
+  static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
+  static_assert(TILE % NW == 0 && NROPE <= NW, "DMA split");
+  static_assert(!ROPE || NHG * PB_HG <= ROPE_BYTES, "Pᵀ in the rope part of a stage");
+  static_assert(!FP8 || (ROPE && __is_same(T, __bf16)), "fp8 rows: head_dim 576, bf16");
+  constexpr int RPL = 2 * ROWS_PER_WAVE;  // fp8 rows: rope bytes per lane per tile (8 or 16)
+  typedef uint32_t ropev __attribute__((ext_vector_type(RPL / 4)));
+  typedef MfmaOps<T> Ops;
+  typedef typename Ops::vec8 vec8;
+
+  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTG * STAGE_BYTES +
+                                                                 (ROPE ? 0 : NHG * PB_HG)];
+  __shared__ float htab[NHG][32];     // per head: rescale factor of the tile / final m
+  __shared__ float xmax[NHG][2][32];  // per head and row half: row max of a tile / final l
+  __shared__ uint32_t rowid[RCH];
+  __shared__ uint32_t tmask[RCH / TILE];
+  __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hg = w >> 2;
+  const int wq = w & 3;
+  const int rh = wq & 1;
+  const int qh = wq >> 1;
+  const int r16 = lane & 15;
+  const int g4 = lane >> 4;                  // 16-lane group
+  const int hl = lane >> 5;
+  const int hq = hg * 32 + 16 * qh + r16;    // softmax head within the m-block
+  const int hp = hg * 32 + (lane & 31);      // P·V head within the m-block
+  const bool has_rope = ROPE && w < NROPE;   // this wave issues rope DMA instruction w
+  const int hblocks = (a.num_heads + MB - 1) / MB;
+  // Kᵀ operand of 16x16x32 (A = 16 rows x 32 dims): row 16rh + r16, dims 32ks + 8g4
+  const int k_row = 16 * rh + r16;
+  const int k_base = ring_row_base(k_row) + 16 * g4;
+  const int rope_k0 = MAIN_BYTES + 16 * ring_rope_slot(k_row, g4);
+  const int rope_k1 = MAIN_BYTES + 16 * ring_rope_slot(k_row, 4 + g4);
+  // Vᵀ operand (ds_read_b64_tr_b16) of k-step kq: the 16-lane group (lane>>4) reads
+  // a 4-row block at dv 128wq + 16*((lane>>4)&1) + 4*(lane&3) (+32d); its first read
+  // (k elements 0..3) takes rows 16kq + 12hl + (lane&15)/4, the second (elements
+  // 4..7) rows 16kq + 8 - 4hl + (lane&15)/4 (lanes 32..63 take their two row blocks
+  // in swapped order, which spreads the Pᵀ writes over all banks).
+  const int tr_col = wq * DVQ * 2 + ((lane >> 4) & 1) * 32 + (lane & 3) * 8;
+  const int tr_r = (lane & 15) >> 2;
+  const int tr00 = ring_row_base(12 * hl + tr_r) + tr_col;
+  const int tr01 = ring_row_base(8 - 4 * hl + tr_r) + tr_col;
+  const int tr10 = ring_row_base(16 + 12 * hl + tr_r) + tr_col;
+  const int tr11 = ring_row_base(24 - 4 * hl + tr_r) + tr_col;
+  // Pᵀ buffer: head h (of the group) at 64 h, its rows in the P·V B-operand order
+  // (k-step kq, lane half hl: chunk 2kq + hl holds rows 16kq + 12hl .. +3 in its
+  // first half and rows 16kq + 8 - 4hl .. +3 in its second); chunk q of head h is
+  // stored at chunk q ^ ((h >> 2) & 3). The wave writes rows 16rh + 4g4 + i of head
+  // 16qh + r16: chunk 2rh + (g4 & 1), half (g4 & 1) ^ (g4 >> 1).
+  const int pw_q = 2 * rh + (g4 & 1);
+  const int pw_off = hg * PB_HG + (16 * qh + r16) * 64 + 16 * (pw_q ^ ((r16 >> 2) & 3)) +
+                     8 * ((g4 & 1) ^ (g4 >> 1));
+  const int pr_head = lane & 31;
+  const int pr_off0 = hg * PB_HG + pr_head * 64 + 16 * ((0 + hl) ^ ((pr_head >> 2) & 3));
+  const int pr_off1 = hg * PB_HG + pr_head * 64 + 16 * ((2 + hl) ^ ((pr_head >> 2) & 3));
+
+  int s2b = a.s2_base;
+  int nfa = a.num_fa;
+  if (a.num_fd == SAS_SCHED_DEVICE) {
+    if (!dev_sched_ok(a, MB)) {
+      if (blockIdx.x == 0) nan_fill<T>(a, tid, NT);
+      return;
+    }
+    s2b = a.metadata[SAS_CFG_OFFSET + 1];
+    nfa = a.metadata[SAS_CFG_OFFSET + 2];  // rows in use (the grid is sized for num_fa)
+  }
+  // XCD-aware row mapping: consecutive FA rows (pieces of one item) share an XCD.
+  const int per_xcd = (nfa + 7) >> 3;
+  const int fa_row = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (fa_row >= nfa || (int)(blockIdx.x >> 3) >= per_xcd) return;
+  const int32_t* fa = a.metadata + fa_row * SAS_FA_METADATA_SIZE;
+  if (fa[0] == 0) return;
+  int b = fa[1], m = fa[2];
+  const int j_start = fa[3];
+  const int b_end = fa[4], s_end = fa[5], j_end = fa[6];
+  int slot = fa[7];
+  const uint32_t kv_base = (uint32_t)(uintptr_t)kv_lds;
+
+  const char* ori_kv = (const char*)a.ori_kv;
+  const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
+  const float sc = a.softmax_scale * LOG2E;
+  if (tid < 2) first_neg[tid] = INT32_MAX;
+  __syncthreads();
+
+  // Sinks of this lane's softmax head in the (at most two) head blocks of an
+  // item, loaded once: a load per item would also wait for the previous item's
+  // output stores (one in-order counter covers loads and stores).
+  const float sink_hb0 = hq < a.num_heads ? a.sinks[hq] : -INFINITY;
+  const float sink_hb1 = MB + hq < a.num_heads ? a.sinks[MB + hq] : -INFINITY;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+  int item_par = 0;  // which first_neg slot the next top-k scan uses
+  bool first_item = true;
+  for (;;) {
+    b = __builtin_amdgcn_readfirstlane(b);
+    m = __builtin_amdgcn_readfirstlane(m);
+    // normalise the cursor: skip batches with no (more) query rows
+    while (b < a.batch && b <= b_end && m >= ld_uniform(a.act_q_lens + b) * hblocks) {
+      ++b;
+      m = 0;
+    }
+    if (b >= a.batch || b > b_end || (b == b_end && m > s_end)) break;
+    const bool is_end = (b == b_end && m == s_end);
+    const int s = m / hblocks;
+    const int hb = m - s * hblocks;
+    if (is_end && j_end == 0) break;
+
+    const int act_q = ld_uniform(a.act_q_lens + b);
+    const int act_kv = ld_uniform(a.seqused_kv + b);
+    const int tok = ld_uniform(a.q_prefix + b) + s;
+    const ItemGeom g =
+        item_geom(act_q, act_kv, s, a.ori_win_left, a.scenario, a.cmp_ratio, a.topk);
+    const int L = g.n_win + g.n_cmp;
+    const int nblk = (L + s2b - 1) / s2b;
+    const int blo = first_item ? j_start : 0;
+    int bhi = is_end ? j_end : nblk;
+    if (bhi > nblk) bhi = nblk;
+    const bool partial = (first_item && j_start > 0) || is_end;
+    const int p_lo = blo * s2b;
+    const int p_hi = bhi * s2b < L ? bhi * s2b : L;
+    const bool tok_ok = tok >= 0 && tok < a.total_tokens;
+
+    // query fragment of the wave's 16 heads (B operand of Sᵀ = K·Qᵀ)
+    i16x8 qf[NKS];
+    // ---- online-softmax state of head hq (golden.py:156-160 seeds m = sink,
+    // l = 1; the 1 goes to the lanes of group 0 of the first row half, whose row
+    // sums are added to the others' at the end) ----
+    const float sink_v = hb == 0 ? sink_hb0 : sink_hb1;
+    const bool hq_ok = hb * MB + hq < a.num_heads;
+    float m_run = partial ? -INFINITY : (hq_ok ? sink_v * LOG2E : -INFINITY);
+    float l_part = (partial || g4 != 0 || rh != 0) ? 0.0f : 1.0f;
+    float mx = -INFINITY;
+    f32x16 acc[DVB];
+#pragma unroll
+    for (int d = 0; d < DVB; ++d)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[d][j] = 0.0f;
+
+    // ---- scenario 3: position of the first -1 among the scanned top-k slots ----
+    // (golden.py:48-53: the scan stops at the first -1). The first chunk's own
+    // top-k loads double as the scan of its range; the slots outside it are
+    // loaded in the same batch, and the block-table loads of the chunk are
+    // issued before the barrier that publishes the result (the -1 cut is
+    // applied when the row ids are packed). The two first_neg slots alternate
+    // between scans, so a slot is reset without a barrier of its own.
+    const int32_t* idx_row =
+        a.cmp_indices ? a.cmp_indices + (size_t)(tok_ok ? tok : 0) * a.topk : nullptr;
+    const bool scan3 = a.scenario == 3 && idx_row != nullptr && a.topk > 0;
+    const int jmax = (scan3 && p_hi > g.n_win) ? min(p_hi - g.n_win, g.n_cmp) : 0;
+    bool stop_pending = jmax > 0;
+    int cmp_stop = g.n_cmp;
+
+    for (int c0 = p_lo; c0 < p_hi; c0 += RCH) {
+      const int clen = (p_hi - c0) < RCH ? (p_hi - c0) : RCH;
+      const int ntile = (clen + TILE - 1) / TILE;
+      // query fragment of the item (first chunk): compiler-visible loads issued
+      // before the resolution's loads, so they land during its memory round
+      // trips; the compiler's wait for the table words below covers them
+      if (c0 == p_lo) {
+        const int head_q = hb * MB + hq;
+        const bool hok = head_q < a.num_heads && tok_ok;
+        const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
+                                                 (hok ? head_q : 0)) * DQK;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          i16x8 v = *(const i16x8*)(qrow + 32 * ks + 8 * g4);
+          qf[ks] = hok ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        }
+      }
+      // ---- resolve positions -> cache rows (bit 31: compressed cache) ----
+      constexpr int PER = RCH / NT;
+      static_assert(PER == 2 || PER == 4, "resolution positions per thread");
+      int cid[PER];
+      int tab[PER];
+      const int own_lo = max(c0 - g.n_win, 0);
+      const int own_hi = min(max(c0 + clen - g.n_win, own_lo), jmax);
+      const int n_extra = stop_pending ? jmax - (own_hi - own_lo) : 0;
+      constexpr int SCAN_PER = 4;
+      auto extra_slot = [&](int x) { return x < own_lo ? x : x + (own_hi - own_lo); };
+      int sv0[SCAN_PER];
+      if (scan3) {
+        // all loads issued, then one wait that also ties their destinations
+        int v[PER];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int jj = c0 + e * NT + tid - g.n_win;
+          const int32_t* src = idx_row + (jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1));
+          asm volatile("global_load_dword %0, %1, off" : "=v"(v[e]) : "v"(src) : "memory");
+        }
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) {
+          const int x = e * NT + tid;  // clamped into range; unused when n_extra == 0
+          const int xc = x < n_extra ? x : (n_extra > 0 ? n_extra - 1 : 0);
+          const int32_t* src = idx_row + (n_extra > 0 ? extra_slot(xc) : 0);
+          asm volatile("global_load_dword %0, %1, off" : "=v"(sv0[e]) : "v"(src) : "memory");
+        }
+        if constexpr (PER == 4) {
+          asm volatile("s_waitcnt vmcnt(0)"
+                       : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(sv0[0]),
+                         "+v"(sv0[1]), "+v"(sv0[2]), "+v"(sv0[3])
+                       :
+                       : "memory");
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)"
+                       : "+v"(v[0]), "+v"(v[1]), "+v"(sv0[0]), "+v"(sv0[1]), "+v"(sv0[2]),
+                         "+v"(sv0[3])
+                       :
+                       : "memory");
+        }
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int r = e * NT + tid;
+          const int pos = c0 + r;
+          cid[e] = (r < clen && tok_ok && pos >= g.n_win) ? v[e] : -1;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int r = e * NT + tid;
+          const int pos = c0 + r;
+          cid[e] = (r < clen && tok_ok && pos >= g.n_win) ? pos - g.n_win : -1;
+        }
+      }
+      if (stop_pending) {
+        int mine = g.n_cmp;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int jj = c0 + e * NT + tid - g.n_win;
+          if (jj >= 0 && jj < jmax && e * NT + tid < clen && cid[e] == -1 && jj < mine) mine = jj;
+        }
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) {
+          const int x = e * NT + tid;
+          if (x < n_extra && sv0[e] == -1 && extra_slot(x) < mine) mine = extra_slot(x);
+        }
+        for (int x0 = NT * SCAN_PER; x0 < n_extra; x0 += NT * SCAN_PER) {  // beyond the first round
+          int v[SCAN_PER];
+#pragma unroll
+          for (int e = 0; e < SCAN_PER; ++e) {  // unconditional, clamped: all loads in flight at once
+            const int x = x0 + e * NT + tid;
+            v[e] = idx_row[extra_slot(x < n_extra ? x : n_extra - 1)];
+          }
+#pragma unroll
+          for (int e = 0; e < SCAN_PER; ++e) {
+            const int x = x0 + e * NT + tid;
+            if (x < n_extra && v[e] == -1 && extra_slot(x) < mine) mine = extra_slot(x);
+          }
+        }
+        if (mine < g.n_cmp) atomicMin(&first_neg[item_par], mine);
+      }
+      // block-table words (compiler-visible loads with in-bounds addresses)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int r = e * NT + tid;
+        const int pos = c0 + r;
+        const bool win = pos < g.n_win;
+        const int key = win ? g.win_lo + pos : cid[e];
+        const int bsz = win ? a.ori_block_size : a.cmp_block_size;
+        const int tlen = win ? a.ori_table_len : a.cmp_table_len;
+        const int32_t* tbl = win ? a.ori_block_table : a.cmp_block_table;
+        const int bi = key >= 0 ? key / bsz : 0;
+        const bool ok = r < clen && tok_ok && key >= 0 && bi < tlen && (win || cid[e] < g.thr);
+        const int t = (tbl != nullptr) ? tbl[(size_t)b * tlen + (bi < tlen ? bi : tlen - 1)] : -1;
+        tab[e] = ok ? t : -1;
+      }
+      // every load so far (table words, query fragment) has landed, as the compiler sees it
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+      if (stop_pending) {
+        __syncthreads();  // every thread's atomicMin is in
+        cmp_stop = min(first_neg[item_par], g.n_cmp);
+        if (tid == 0) first_neg[item_par ^ 1] = INT32_MAX;  // the next scan's slot
+        item_par ^= 1;
+        stop_pending = false;
+      }
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int r = e * NT + tid;
+        const int pos = c0 + r;
+        uint32_t id = ROW_INVALID;
+        const int phys = tab[e];
+        if (r < clen && tok_ok && phys >= 0) {
+          if (pos < g.n_win) {
+            if (phys < a.ori_block_num)
+              id = (uint32_t)(phys * a.ori_block_size + (g.win_lo + pos) % a.ori_block_size);
+          } else if (phys < a.cmp_block_num && (!scan3 || pos - g.n_win < cmp_stop)) {
+            id = (uint32_t)(phys * a.cmp_block_size + cid[e] % a.cmp_block_size) | 0x80000000u;
+          }
+        }
+        rowid[r] = id;  // masked rows are read from the zero row
+        const unsigned long long bal = __ballot(id != ROW_INVALID);
+        if (lane == 0) {
+          tmask[(r - lane) / TILE] = (uint32_t)bal;
+          tmask[(r - lane) / TILE + 1] = (uint32_t)(bal >> 32);
+        }
+      }
+      __syncthreads();
+
+      // ---- DMA issue for one tile into one ring stage ----
+      // main part: wave w fills rows w, w + NW, ...; one 1 KB row per instruction
+      // rope part: instruction i (wave i < NROPE) fills rows 8i..8i+7 (8 lanes per row)
+      auto row_ptr = [&](uint32_t id) -> const char* {
+        const char* base = (id & 0x80000000u) ? cmp_kv : ori_kv;
+        const char* p = base + (size_t)(id & 0x7FFFFFFFu) * ROWB;
+        return id == ROW_INVALID ? (const char*)g_zero_row : p;
+      };
+      auto lane_row = [&](uint64_t ptrs, int j) -> const char* {
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ptrs, j);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(ptrs >> 32), j);
+        return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+      };
+      // The DMAs of one tile: the row addresses are gathered first (next_addrs),
+      // then instruction j goes out with dma_one(j), so the instructions can be
+      // spread between MFMAs.
+      struct DmaAddrs {
+        uint64_t main;     // lane j < ROWS_PER_WAVE: this wave's j-th main row
+        const char* rope;  // per lane: its 16-byte rope piece (waves w < NROPE)
+        uint32_t sbase;
+      };
+      // Addresses of the DMAs of tile t. Past the chunk's last tile the
+      // instructions read the zero row into the stage they would fill, which
+      // nothing reads before the chunk ends (keeps the vmcnt accounting uniform).
+      auto next_addrs = [&](int tile) -> DmaAddrs {
+        DmaAddrs d;
+        const bool real = tile < ntile;
+        d.sbase = kv_base + (tile % NSTG) * STAGE_BYTES;
+        const int t0 = real ? tile : 0;
+        d.main = (uint64_t)(uintptr_t)row_ptr(
+            rowid[t0 * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
+        d.rope = (const char*)g_zero_row;
+        if constexpr (ROPE) {
+          const int r = 8 * (w < NROPE ? w : 0) + (lane >> 3);  // rope instruction w: rows 8w..8w+7
+          const int cr = (lane & 7) ^ ((r >> 1) & 7);           // the chunk slot lane & 7 holds
+          d.rope = row_ptr(rowid[t0 * TILE + r]) + 1024 + cr * 16;
+        }
+        if (!real) {
+          d.main = (uint64_t)(uintptr_t)g_zero_row;
+          d.rope = (const char*)g_zero_row;
+        }
+        return d;
+      };
+      auto dma_one = [&](const DmaAddrs& d, int j) {
+        if (j < ROWS_PER_WAVE) {
+          const int r = w + NW * j;
+          dma16_sbase(lane_row(d.main, j), (uint32_t)lane * 16u, d.sbase + ring_row_base(r));
+        } else if constexpr (ROPE) {
+          if (has_rope) dma16_vaddr(d.rope, d.sbase + MAIN_BYTES + w * 1024);
+        }
+      };
+      auto issue = [&](const DmaAddrs& d) {
+#pragma unroll
+        for (int j = 0; j < DMA_MAX; ++j) dma_one(d, j);
+      };
+      // this wave's DMAs of all but the newest tile have landed
+      auto wait_all_but_one_tile = [&]() {
+        if (has_rope) wait_vmcnt<ROWS_PER_WAVE + 1>();
+        else wait_vmcnt<ROWS_PER_WAVE>();
+      };
+
+      // ---- fp8 rows: VGPR loads, then dequantize into one ring stage ----
+      // wave w takes rows w + NW j (j < ROWS_PER_WAVE): lane l loads bytes 8l..8l+7
+      // (dims 8l..8l+7, scale l / 16) of each, and RPL rope bytes of row
+      // w + NW (l / (128 / RPL)).
+      struct Fp8Tile {
+        uint2 v[ROWS_PER_WAVE];
+        float s[ROWS_PER_WAVE];
+        ropev rope;
+      };
+      constexpr int ROPE_LPR = 128 / RPL;  // lanes per row for the rope bytes
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      auto fp8_load = [&](Fp8Tile& f, int tile) {
+        const uint64_t my_ptrs = (uint64_t)(uintptr_t)row_ptr(
+            rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
+        const char* rp = nullptr;
+#pragma unroll
+        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
+          const char* p = lane_row(my_ptrs, j);
+          const u32x2 t = __builtin_nontemporal_load((const SAS_GLOBAL u32x2*)(p + 8 * lane));
+          f.v[j] = make_uint2(t[0], t[1]);
+          f.s[j] = __builtin_nontemporal_load((const SAS_GLOBAL float*)(p + 512 + 4 * (lane >> 4)));
+          rp = (lane / ROPE_LPR == j) ? p : rp;
+        }
+        f.rope = __builtin_nontemporal_load(
+            (const SAS_GLOBAL ropev*)(rp + ROPE_OFF + (lane % ROPE_LPR) * RPL));
+      };
+      auto fp8_store = [&](const Fp8Tile& f, int tile) {
+        unsigned char* sb = kv_lds + (tile % NSTG) * STAGE_BYTES;
+#pragma unroll
+        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
+          const int r = w + NW * j;
+          *(i16x8*)(sb + ring_row_base(r) + 16 * lane) = fp8x8_dequant_bf16(f.v[j], f.s[j]);
+        }
+        // the lane's RPL rope bytes: whole 16-byte chunks (RPL 16; consecutive chunks
+        // of a row need not be adjacent in the rotated rope layout, so one store
+        // each) or half of one (RPL 8)
+        const int r = w + NW * (lane / ROPE_LPR);
+        const int b0 = (lane % ROPE_LPR) * RPL;  // byte offset within the row's rope
+        if constexpr (RPL >= 16) {
+          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+          for (int k = 0; k < RPL / 16; ++k)
+            *(u32x4*)(sb + MAIN_BYTES + ring_rope_slot(r, b0 / 16 + k) * 16) =
+                (u32x4){f.rope[4 * k], f.rope[4 * k + 1], f.rope[4 * k + 2], f.rope[4 * k + 3]};
+        } else {
+          static_assert(RPL == 8, "rope bytes per lane");
+          *(u32x2*)(sb + MAIN_BYTES + ring_rope_slot(r, b0 / 16) * 16 + (b0 & 8)) =
+              (u32x2){f.rope[0], f.rope[1]};
+        }
+      };
+      Fp8Tile fpt;
+
+      typedef const unsigned char SAS_LDS* lds_p;
+      auto stage_of = [&](int tile) -> lds_p {
+        return (lds_p)(kv_base + (uint32_t)((tile % NSTG) * STAGE_BYTES));
+      };
+      auto pbuf_of = [&](int tile) -> uint32_t {
+        return ROPE ? kv_base + (uint32_t)((tile % NSTG) * STAGE_BYTES + MAIN_BYTES)
+                    : kv_base + (uint32_t)(NSTG * STAGE_BYTES);
+      };
+      // K operand of k-step ks (the wave's 16 rows) from stage sb
+      auto kop = [&](lds_p sb, int ks) -> i16x8 {
+        const lds_p p = ks < NKS_MAIN ? sb + k_base + 64 * ks
+                                      : sb + (ks == NKS_MAIN ? rope_k0 : rope_k1);
+        return *(const i16x8 SAS_LDS*)p;
+      };
+      auto mma16 = [&](i16x8 x, i16x8 y, f32x4 c) -> f32x4 {
+        return __is_same(T, __bf16)
+                   ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(vec8, x),
+                                                             __builtin_bit_cast(vec8, y), c, 0, 0, 0)
+                   : __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vec8, x),
+                                                            __builtin_bit_cast(vec8, y), c, 0, 0, 0);
+      };
+      // row max of a tile's scores over this wave's rows (lanes l, l^16, l^32,
+      // l^48 hold the wave's 16 rows of the lane's head); rows the tile mask
+      // marks invalid become -inf first
+      auto row_max = [&](f32x4& x, int tile) -> float {
+        const uint32_t tm = tmask[tile];
+        if (__builtin_amdgcn_readfirstlane(tm) != 0xFFFFFFFFu) {
+          const uint32_t vm = tm >> (16 * rh + 4 * g4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = ((vm >> i) & 1u) ? x[i] : -INFINITY;
+        }
+        float mm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+        const auto r1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mm),
+                                                         __float_as_uint(mm), false, false);
+        mm = fmaxf(__uint_as_float(r1[0]), __uint_as_float(r1[1]));
+        mm = wave_max_pair(mm);
+        if (g4 == 0) xmax[hg][rh][16 * qh + r16] = mm;
+        return mm;
+      };
+
+      // ---- prologue: tiles 0, 1, 2 in flight, Q·Kᵀ of tile 0 ----
+      if constexpr (FP8) {
+        // one tile's registers at a time (the loop holds one tile in flight too)
+        fp8_load(fpt, 0);
+        fp8_store(fpt, 0);
+        if (ntile > 1) {
+          fp8_load(fpt, 1);
+          fp8_store(fpt, 1);
+        }
+      } else {
+        issue(next_addrs(0));
+        issue(next_addrs(1));
+        issue(next_addrs(2));
+        wait_all_but_one_tile();  // tiles 0 and 1 have landed (tile 2 may be in flight)
+      }
+      __syncthreads();
+      f32x4 st;
+      {
+        const lds_p sb = stage_of(0);
+        f32x4 ce = {0.0f, 0.0f, 0.0f, 0.0f}, co = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks += 2) {
+          ce = mma16(kop(sb, ks), qf[ks], ce);
+          co = mma16(kop(sb, ks + 1), qf[ks + 1], co);
+        }
+        st = ce + co;
+        const float own = row_max(st, 0);
+        __syncthreads();
+        mx = fmaxf(own, xmax[hg][rh ^ 1][16 * qh + r16]);
+      }
+      DmaAddrs nd;
+      if constexpr (!FP8) nd = next_addrs(3);
+
+      for (int it = 0; it < ntile; ++it) {
+        const lds_p sb = stage_of(it);
+        const uint32_t pb = pbuf_of(it);
+        if constexpr (FP8) {
+          if (it + 2 < ntile) fp8_load(fpt, it + 2);
+        }
+        // ---- phase A: softmax of tile it between the Q·Kᵀ MFMAs of tile it + 1 ----
+        // (st holds tile it's scores, masked by row_max; mx its tile max)
+        f32x4 sn;
+        float own = -INFINITY;
+        auto phase_a = [&](auto with_qk) {
+          constexpr bool QK = decltype(with_qk)::value;
+          constexpr int KPF = FP8 ? 3 : 6;
+          const lds_p sbn = stage_of(it + 1);
+          i16x8 kb[KPF];
+          f32x4 ce = {0.0f, 0.0f, 0.0f, 0.0f}, co = {0.0f, 0.0f, 0.0f, 0.0f};
+          if constexpr (QK) {
+#pragma unroll
+            for (int i = 0; i < KPF; ++i) kb[i] = kop(sbn, i);
+          }
+          float p[4], alpha = 1.0f, m_sub = 0.0f;
+          i16x4 pk;
+          // softmax of tile it in slices: slice k runs after k-step k's MFMA
+          auto slice = [&](int k) {
+            if (k == 0) {
+              const float mt = mx * sc;
+              const bool grow = mt > m_run;
+              const float m_new = grow ? mt : m_run;
+              alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // -inf -> 0
+              m_run = m_new;
+              l_part *= alpha;
+              // a head with no key and no sink yet (m_run = -inf) has every score
+              // -inf: subtracting 0 instead keeps its P at exactly 0
+              m_sub = m_new == -INFINITY ? 0.0f : m_new;
+            } else if (k == 1) {
+              // both row halves hold the same factor: the first writes it
+              if (g4 == 0 && rh == 0) htab[hg][16 * qh + r16] = alpha;
+            } else if (k == 2 || k == 3) {
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const int i = 2 * (k - 2) + e;
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[i], sc, -m_sub));
+              }
+            } else if (k == 4) {
+              l_part += (p[0] + p[1]) + (p[2] + p[3]);
+              pk = (i16x4){Ops::from_f32(p[0]), Ops::from_f32(p[1]), Ops::from_f32(p[2]),
+                           Ops::from_f32(p[3])};
+            } else if (k == 5) {
+              *(i16x4 SAS_LDS*)(pb + pw_off) = pk;
+            }
+          };
+          constexpr int DMA_AT = 6;  // first k-step with a DMA after it
+          constexpr int NSTEP = NKS > DMA_AT + DMA_MAX ? NKS : DMA_AT + DMA_MAX;
+#pragma unroll
+          for (int ks = 0; ks < NSTEP; ++ks) {
+            if constexpr (QK) {
+              if (ks < NKS) {
+                const i16x8 k0 = kb[ks % KPF];
+                if (ks + KPF < NKS) kb[ks % KPF] = kop(sbn, ks + KPF);
+                if (ks & 1) co = mma16(k0, qf[ks], co);
+                else ce = mma16(k0, qf[ks], ce);
+              }
+            }
+            slice(ks);
+            // DMA instruction j of tile it + 3 after k-step DMA_AT + j
+            if constexpr (!FP8) {
+#pragma unroll
+              for (int j = 0; j < DMA_MAX; ++j)
+                if (j + DMA_AT == ks) dma_one(nd, j);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          if constexpr (QK) {
+            sn = ce + co;
+            own = row_max(sn, it + 1);
+          }
+        };
+        if (it + 1 < ntile) phase_a(std::true_type{});
+        else phase_a(std::false_type{});
+        __syncthreads();  // barrier 1: Pᵀ, factors of tile it and row maxima of it + 1 in LDS
+        DmaAddrs nd4;
+        if constexpr (!FP8) nd4 = next_addrs(it + 4);  // (rowid reads under P·V)
+
+        // ---- phase B: Oᵀ = alpha·Oᵀ + Vᵀ·Pᵀ over both 16-row k-steps ----
+        {
+          if (it + 1 < ntile) mx = fmaxf(own, xmax[hg][rh ^ 1][16 * qh + r16]);
+          constexpr int VPF = FP8 ? 2 : SAS_VPF;
+          constexpr int NPV = 2 * DVB;
+          const float al = htab[hg][lane & 31];
+          const i16x8 pq0 = *(const i16x8 SAS_LDS*)(pb + pr_off0);
+          const i16x8 pq1 = *(const i16x8 SAS_LDS*)(pb + pr_off1);
+          typedef i16x4 SAS_LDS* lds4;
+          // MFMA i: dv block i % DVB, k-step i / DVB (independent accumulators back to back)
+          auto vop = [&](int i) -> i16x8 {
+            const int d = i % DVB, kq = i / DVB;
+            const i16x4 g0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds4)(sb + (kq ? tr10 : tr00) + d * 64));
+            const i16x4 g1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds4)(sb + (kq ? tr11 : tr01) + d * 64));
+            return (i16x8){g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+          };
+          i16x8 vbuf[VPF];
+#pragma unroll
+          for (int i = 0; i < VPF; ++i) vbuf[i] = vop(i);
+#pragma unroll
+          for (int i = 0; i < NPV; ++i) {
+            const int d = i % DVB, kq = i / DVB;
+            if (kq == 0) {
+#pragma unroll
+              for (int j = 0; j < 16; ++j) acc[d][j] *= al;
+            }
+            const i16x8 aop = vbuf[i % VPF];
+            if (i + VPF < NPV) vbuf[i % VPF] = vop(i + VPF);
+            acc[d] = Ops::mma(aop, kq ? pq1 : pq0, acc[d]);
+          }
+        }
+        if constexpr (FP8) {
+          // tile it + 2 into its stage (tile it - 2's, free since barrier 2 of it - 2)
+          if (it + 2 < ntile) fp8_store(fpt, it + 2);
+        } else {
+          // this wave's share of tile it + 2 has landed (tile it + 3's may be in flight)
+          wait_all_but_one_tile();
+        }
+        __syncthreads();  // barrier 2: tile it + 2 in LDS; stage it and its Pᵀ free
+        if constexpr (!FP8) nd = nd4;
+        st = sn;
+      }
+      if constexpr (!FP8) {
+        wait_vmcnt<0>();  // the last (zero-row) DMAs have landed ...
+        __syncthreads();  // ... for every wave, before LDS is reused
+      }
+    }
+
+    // ---- row sums of head hq over the wave's four lanes and both row halves;
+    // (m, l) to the P·V layout (head hp = hg * 32 + lane % 32) ----
+    {
+      const auto r1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_part),
+                                                       __float_as_uint(l_part), false, false);
+      const float l16 = __uint_as_float(r1[0]) + __uint_as_float(r1[1]);
+      const float lq = wave_sum_pair(l16);
+      if (g4 == 0) {
+        xmax[hg][rh][16 * qh + r16] = lq;
+        if (rh == 0) htab[hg][16 * qh + r16] = m_run;
+      }
+    }
+    __syncthreads();
+    const float m_fin = htab[hg][lane & 31];
+    const float l_run = xmax[hg][0][lane & 31] + xmax[hg][1][lane & 31];
+    const bool head_p_ok = hb * MB + hp < a.num_heads;
+
+    // ---- epilogue: the item's rows go out through LDS (the ring is free), so
+    // every store instruction writes whole rows ----
+    {
+      unsigned char* stg = kv_lds;
+      const int nh = min(MB, a.num_heads - hb * MB);  // heads of this item
+      int tid_e = tid, hl_e = hp, dv_e = wq * DVQ + 4 * hl;
+      asm volatile("" : "+v"(tid_e), "+v"(hl_e), "+v"(dv_e));
+      if (!partial) {
+        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes)
+        constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
+        static_assert(MB * SROW <= NSTG * STAGE_BYTES, "output staging");
+        const float inv = 1.0f / l_run;
+#pragma unroll
+        for (int d = 0; d < DVB; ++d)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int dv = dv_e + 32 * d + 8 * q4;
+            const i16x4 v = {Ops::from_f32(acc[d][4 * q4] * inv),
+                             Ops::from_f32(acc[d][4 * q4 + 1] * inv),
+                             Ops::from_f32(acc[d][4 * q4 + 2] * inv),
+                             Ops::from_f32(acc[d][4 * q4 + 3] * inv)};
+            *(i16x4*)(stg + hl_e * SROW + dv * 2) = v;
+          }
+        __syncthreads();
+        if (tok_ok) {
+          char* obase = (char*)((T*)a.out + ((size_t)tok * a.num_heads + hb * MB) * DV);
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            *(i16x8*)(obase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
+          }
+          if (wq == 0 && hl == 0 && head_p_ok)
+            a.lse[(size_t)tok * a.num_heads + hb * MB + hl_e] = (m_fin + __log2f(l_run)) * LN2;
+        }
+      } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
+        // fp32 partials (acc / l), staged one dv half (waves wq = 2 half, 2 half + 1) at a time
+        constexpr int HALF = DV / 2;
+        constexpr int SROW = HALF * 4 + 16;
+        constexpr int CPR = HALF * 4 / 16;
+        static_assert(MB * SROW <= NSTG * STAGE_BYTES, "partial staging");
+        const bool empty = !(l_run > 0.0f);
+        const float inv = empty ? 0.0f : 1.0f / l_run;
+        char* wbase = (char*)(a.workspace + (size_t)slot * MB * DV);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          if (half) __syncthreads();  // the first half has been read out
+          if ((wq >> 1) == half) {
+#pragma unroll
+            for (int d = 0; d < DVB; ++d)
+#pragma unroll
+              for (int q4 = 0; q4 < 4; ++q4) {
+                const int dv = dv_e - half * HALF + 32 * d + 8 * q4;  // within the half
+                f32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[d][4 * q4 + e] * inv;
+                *(f32x4*)(stg + hl_e * SROW + dv * 4) = v;
+              }
+          }
+          __syncthreads();
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            *(f32x4*)(wbase + ((size_t)h * DV + half * HALF) * 4 + c16 * 16) =
+                *(const f32x4*)(stg + h * SROW + c16 * 16);
+          }
+        }
+        if (wq == 0 && hl == 0 && head_p_ok) {
+          float* wl = a.workspace + (size_t)a.num_partial_slots * MB * DV;
+          wl[(size_t)slot * MB + hl_e] = empty ? -INFINITY : (m_fin + __log2f(l_run)) * LN2;
+        }
+      }
+    }
+    __syncthreads();  // the staging area and the head tables are read out before the next item
+    if (partial) ++slot;
+    if (is_end) break;
+    first_item = false;
+    ++m;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Split-KV merge: lse = log(e^sink + Σ e^lse_i), out = Σ e^(lse_i - lse) o_i
 // ---------------------------------------------------------------------------
 // Grid: (merge task, group of MERGE_HPB heads). Thread t owns head t / 32 of
@@ -1051,11 +1830,17 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
 
 template <int DQK, int NHG, typename T, int KVF>
 static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
-  const int phases = a.phases == 0 ? 3 : a.phases;
+  const int phases = (a.phases & 3) == 0 ? 3 : (a.phases & 3);
   if (phases & 1) {
     const int per_xcd = (a.num_fa + 7) / 8;
-    hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
-                       dim3(128 * NHG), 0, st, a);
+    // native rows: one wave per SIMD (attn2_kernel); fp8 rows: the pipelined
+    // two-waves-per-SIMD kernel, whose second wave hides the dequantization
+    if (KVF == SAS_KV_FP8_DS_MLA || (a.phases & SAS_PHASE_PIPELINED))
+      hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
+                         dim3(256 * NHG), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
+                         dim3(128 * NHG), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1123,8 +1908,8 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     set_error("sas_attention_launch: scenario inputs missing");
     return SAS_E_INVALID;
   }
-  if (a->phases < 0 || a->phases > 3) {
-    set_error("sas_attention_launch: phases must be 0..3");
+  if (a->phases < 0 || a->phases > 7) {
+    set_error("sas_attention_launch: phases must be 0..7");
     return SAS_E_INVALID;
   }
   const bool dev_sched = a->num_fd == SAS_SCHED_DEVICE;

@@ -30,7 +30,7 @@ HAS_GPU = torch.cuda.is_available()
 requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
 
 if HAS_GPU:
-    from sparse_attn_sharedkv_amd import sparse_flash_mla
+    from sparse_attn_sharedkv_amd import _lib, api, sparse_flash_mla
     from sparse_attn_sharedkv_amd.kv_fp8 import append_kv_fp8, quantize_kv_fp8
 
 
@@ -162,15 +162,29 @@ def test_fp8_attention_matches_oracle(heads, k, lens, sinks):
     _check(out, lse, kw)
 
 
+def _run_pipelined(kw, **extra):
+    """Native rows through the kernel fp8 rows use (SAS_PHASE_PIPELINED)."""
+    kw = {k: v for k, v in _dev(kw).items() if k != "topk_cmp"}
+    prep = api.prepare(**kw, **extra)
+    api.launch(prep, phases=_lib.SAS_PHASE_PIPELINED)
+    torch.cuda.synchronize()
+    return prep.out.clone(), prep.lse.clone()
+
+
 @requires_gpu
 @pytest.mark.parametrize("cores", [256, 7])
 def test_fp8_equals_bf16_path_on_dequantized_cache(cores):
+    # fp8 rows are dequantized into the same bf16 LDS layout the native rows are
+    # gathered into, so the same kernel on the dequantized cache is bitwise equal
     _say(f"fp8 vs bf16-on-dequantized cores={cores}")
     kw = _fp8_case(lens=[4000, 2999, 3500], heads=128, k=2048, seed=5)
     out8, lse8 = _run(kw, core_num=cores)
-    out16, lse16 = _run(_dequant_kw(kw), core_num=cores)
-    assert torch.equal(out8.cpu(), out16.cpu())
-    assert torch.equal(lse8.cpu(), lse16.cpu())
+    out16, lse16 = _run_pipelined(_dequant_kw(kw), core_num=cores)
+    assert torch.equal(out8.cpu(), out16.reshape(out8.shape).cpu())
+    assert torch.equal(lse8.cpu(), lse16.reshape(lse8.shape).cpu())
+    # the default kernel for native rows agrees to within the accuracy contract
+    out_d, lse_d = _run(_dequant_kw(kw), core_num=cores)
+    _check(out_d, lse_d, _dequant_kw(kw))
 
 
 @requires_gpu
