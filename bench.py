@@ -20,8 +20,11 @@ against HBM or the bf16 MFMA peak, whichever bounds the shape.
 Prints one JSON line. ``value`` is TFLOP/s of the whole call; the
 ``roofline`` object rates the attention kernel alone: algorithmic bytes per
 launch / its mean duration (HIP events around each launch in the timed loop)
-against 8 TB/s HBM. ``cpu_baseline`` times the CPU restatement of the
-reference's golden math on this host over all query rows of one input set.
+against 8 TB/s HBM. ``profiled_counters`` repeats the MFMA / VALU / LDS activity
+of the same kernel and workload from the committed rocprofv3 SQ counter summary
+(``profiles/attn_kernel_<workload>_sq.txt``). ``cpu_baseline`` times the CPU
+restatement of the reference's golden math on this host over query rows of one
+input set.
 """
 
 from __future__ import annotations
@@ -72,6 +75,29 @@ def measured_traffic(workload):
         if line.startswith("traffic_bytes_per_launch:"):
             return int(float(line.split(":", 1)[1]))
     return None
+
+
+def profiled_counters(workload):
+    """MFMA / VALU / LDS activity of the attention kernel from the committed rocprofv3 SQ
+    counter summary (``profiles/attn_kernel_<workload>_sq.txt``), or None."""
+    path = os.path.join(ROOT, "profiles", f"attn_kernel_{workload}_sq.txt")
+    if not os.path.exists(path):
+        return None
+    out = {}
+    for line in open(path, encoding="utf-8"):
+        if ":" in line and not line.startswith("#"):
+            key, val = line.split(":", 1)
+            key = key.strip()
+            if key in ("mfma_busy_frac", "valu_active_frac", "lds_active_frac",
+                       "valu_insts_per_wave_per_tile", "lds_bank_conflict_frac"):
+                try:
+                    out[key] = float(val.split()[0])
+                except ValueError:
+                    pass
+    if not out:
+        return None
+    out["source"] = os.path.relpath(path, ROOT)
+    return out
 
 
 def cpu_baseline(inputs, counts, max_tokens=64):
@@ -191,6 +217,8 @@ def main():
     srt = attn_ms
 
     achieved = nbytes / (attn_avg * 1e-3) / 1e9
+    # native rows run on the one-wave-per-SIMD kernel, fp8 rows on the pipelined one
+    kernel = "sas::attn3_kernel" if sets[0].get("kv_cache_dtype") else "sas::attn2_kernel"
     if w.get("prefill"):
         # prefill: consecutive query rows re-read each other's cache rows, which
         # stay on chip; the algorithmic HBM bytes are q, out and lse once plus the
@@ -203,20 +231,20 @@ def main():
             roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
                     "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(pbytes),
-                    "kernel": "sas::attn_kernel"}
+                    "kernel": kernel}
         else:
             ach = flops / (attn_avg * 1e-3) / 1e12
             roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
                     "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(pbytes),
-                    "kernel": "sas::attn_kernel"}
+                    "kernel": kernel}
         roof["hbm_time_us"] = round(t_hbm * 1e6, 1)
         roof["mfma_time_us"] = round(t_mfma * 1e6, 1)
     else:
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                 "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(nbytes),
-                "kernel": "sas::attn_kernel"}
+                "kernel": kernel}
     res = {
         "metric": METRIC,
         "value": round(flops / (ms_step * 1e-3) / 1e12, 3),
@@ -251,6 +279,9 @@ def main():
         "roofline": roof,
         "peaks": {"hbm_GBps": HBM_PEAK_GBPS, "bf16_mfma_TFLOPs": BF16_PEAK_TFLOPS},
     }
+    prof = profiled_counters(args.workload)
+    if prof is not None:
+        res["profiled_counters"] = prof
     if args.workload in REFERENCE_PUBLISHED:
         res["reference_published"] = REFERENCE_PUBLISHED[args.workload]
     if not args.no_cpu_baseline:

@@ -727,19 +727,20 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
             for (int e = 0; e < 4; ++e) sv[4 * j + e] = st[4 * j + e] + o[j][e];
         }
         // ---- online softmax (exp2 domain) on rows 8(i/4) + 4hl + i%4 ----
-        // (masking only on tiles with invalid rows: tile tails, -1 / out-of-range ids)
+        // (masking only on tiles with invalid rows: tile tails, -1 / out-of-range ids;
+        // the empty asm keeps this a branch, so full tiles skip the selects)
         if (__builtin_amdgcn_readfirstlane(tmask[it]) != 0xFFFFFFFFu) {
+          asm volatile("");
 #pragma unroll
           for (int i = 0; i < 16; ++i)
             sv[i] = ((vm >> (8 * (i / 4) + (i % 4))) & 1u) ? sv[i] : -INFINITY;
         }
+        // max of the raw scores, then scaled: rounding is monotonic, so this is
+        // the max of the scaled scores
         float mloc = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          sv[i] = sv[i] * sc;
-          mloc = fmaxf(mloc, sv[i]);
-        }
-        mloc = wave_max_pair(mloc);
+        for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, sv[i]);
+        mloc = wave_max_pair(mloc) * sc;
         const bool grow = mloc > m_run;
         const float m_new = grow ? mloc : m_run;
         const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // -inf -> 0
@@ -751,7 +752,7 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
         i16x8 pk[2];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float p = __builtin_amdgcn_exp2f(sv[i] - m_sub);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], sc, -m_sub));
           l_part += p;
           pk[i / 8][i % 8] = Ops::from_f32(p);
         }
