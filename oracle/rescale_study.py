@@ -4,8 +4,9 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): a CPU study, no GPU.
 
 For each random configuration of the GPU sweep (``gen.random_sweep_cfg``, the
 reference's U(-10, 10) inputs) it computes golden (``golden_ref``, 512-row
-tiles), the float64 closed form, golden with 32-row tiles, and the kernel's
-order (``kernel_order``) for several thresholds ``tau`` and stream counts, and
+tiles), the float64 closed form, golden with 32- and 64-row tiles, and the
+kernel's order (``kernel_order``) for several step sizes, thresholds ``tau``
+and stream counts, and
 reports per variant how many configurations fail the reference's rule
 (>= 99.5 % of elements within rtol 2^-7 / atol 1e-4 of golden) and how many
 have elements beyond atol = rtol = 2e-2 of golden.
@@ -28,8 +29,10 @@ from . import gen
 from .golden_ref import attend_token, sparse_attn_exact, sparse_attn_oracle
 from .kernel_order import compare, sparse_attn_kernel_order
 
-# (name, tile, tau, streams); "golden32" is golden's own algorithm at 32-row tiles
-VARIANTS = [("golden32", 32, None, 1)] + [(f"tau{t}", 32, float(t), 1) for t in (0, 1, 2, 4, 8)] + \
+# (name, tile, tau, streams); "golden32" / "golden64" are golden's own algorithm at
+# 32- / 64-row tiles; "t64_tau0" is the kernel's order (64-row softmax steps, eager max)
+VARIANTS = [("golden32", 32, None, 1), ("golden64", 64, None, 1), ("t64_tau0", 64, 0.0, 1),
+            ("t64_tau8", 64, 8.0, 1)] + [(f"tau{t}", 32, float(t), 1) for t in (0, 1, 2, 4, 8)] + \
            [("tau0_s2", 32, 0.0, 2), ("tau8_s2", 32, 8.0, 2)]
 
 

@@ -18,8 +18,9 @@
 //         d_qk with v_mfma_f32_32x32x16 (A = K rows from LDS, B = Qᵀ held in
 //         AGPRs); the two partials of a head group meet through LDS, so both
 //         waves hold the same full Sᵀ.
-//   softmax: exp2 domain on 16 rows x 1 head per lane, in registers; the
-//         running max moves at every tile whose max exceeds it.
+//   softmax: exp2 domain on 32 rows (two tiles) x 1 head per lane, in
+//         registers; the running max moves at every 64-row step whose max
+//         exceeds it.
 //   P·V:  each wave accumulates Oᵀ[its dv half x 32 heads] (A = Vᵀ via
 //         ds_read_b64_tr_b16 from the row-major tile, B = Pᵀ straight from the
 //         Sᵀ registers).
@@ -67,6 +68,9 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 #ifndef SAS_KPF
 #define SAS_KPF 8  // K operand reads in flight per wave (attn2_kernel)
+#endif
+#ifndef SAS_PV_SPREAD
+#define SAS_PV_SPREAD 0  // P·V MFMA order of the rescaling tile (attn2_kernel)
 #endif
 #ifndef SAS_VPF
 #define SAS_VPF 4  // Vᵀ operands in flight per wave (attn2_kernel)
@@ -222,30 +226,27 @@ __device__ inline i16x8 fp8x8_dequant_bf16(uint2 v, float s) {
 //   exchange: the two partials of a head group meet through LDS; each wave
 //         adds the other's to its own (fp32 addition is commutative, so both
 //         hold the identical Sᵀ and take identical softmax decisions);
-//   softmax: 16 rows x 1 head per lane, exp2 domain. A head's running max
-//         moves at every tile whose max exceeds it (golden.py:187-191's rule
-//         at 32-row tiles), so the largest score seen so far has P = 1 exactly
-//         when P is rounded to the input type (golden.py:192-196);
+//   softmax: two tiles (64 rows) per step, 32 rows x 1 head per lane, exp2
+//         domain. A head's running max moves at every step whose max exceeds
+//         it (golden.py:187-191's rule at 64-row tiles), so the largest score
+//         seen so far has P = 1 exactly when P is rounded to the input type
+//         (golden.py:192-196); the accumulator rescale is paid once per step;
 //   P·V:  Oᵀ[dv half dh (256) x 32 heads] += Vᵀ·Pᵀ. Pᵀ is taken straight from
 //         the Sᵀ registers: the accumulator holds rows 8(i/4) + 4(lane/32) +
 //         i%4 in element i, which is the B-operand order of the Vᵀ reads
 //         (k-step kq = elements 8kq..8kq+7).
-// Per tile: barrier 1 (partials written) and barrier 2 (the stage is free and
-// the next tile has landed). Ring of 3 stages: tile t + 2 is issued at the
-// head of iteration t into the stage barrier 2 of iteration t - 1 released,
-// and waited for at the end of iteration t + 1 (two iterations in flight).
-// fp8 rows (KVF = SAS_KV_FP8_DS_MLA): tile t + 2 is loaded into VGPRs at the
-// head of iteration t and dequantized into its stage (the same bf16 layout)
-// before barrier 2 of iteration t, so every read of a stage is the bf16 one.
+// Per step (tiles a, b): barrier 1a (b landed, partials of a written), barrier
+// 1b (partials of b written), barrier X (stage a free) and barrier 2 (stage b
+// free, a + 2 landed). Ring of 3 stages: tile a + 2 is issued under the Q·Kᵀ
+// of a into the stage tile a - 1 left, a + 3 under the P·V of b into stage a.
+// Native rows only: fp8 rows run on attn3_kernel.
 template <int DQK, int DV, int NHG, typename T, int KVF>
 __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   constexpr int NW = 2 * NHG;            // waves per workgroup
   constexpr int MB = 32 * NHG;           // heads per item (m-block)
   constexpr int NT = 64 * NW;            // threads
   constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
-  constexpr bool FP8 = KVF == SAS_KV_FP8_DS_MLA;
-  constexpr int ROWB = FP8 ? SAS_FP8_ROW_BYTES : DQK * 2;  // bytes per cache row in HBM
-  constexpr int ROPE_OFF = FP8 ? 528 : 1024;               // byte offset of the rope dims
+  constexpr int ROWB = DQK * 2;          // bytes per cache row in HBM
   constexpr int NKS_MAIN = 16;           // k-steps over the 256 main dims of a half
   constexpr int NKS = NKS_MAIN + (ROPE ? 2 : 0);
   constexpr int DVB = DV / 2 / 32;       // 32-wide dv blocks per wave (8)
@@ -261,13 +262,11 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
   static_assert(TILE % NW == 0 && NROPE % NW == 0, "DMA split");
   static_assert(DMA_PER_TILE <= 63, "vmcnt range");
-  static_assert(!FP8 || (ROPE && __is_same(T, __bf16)), "fp8 rows: head_dim 576, bf16");
-  constexpr int RPL = 2 * ROWS_PER_WAVE;  // fp8 rows: rope bytes per lane per tile (16 or 32)
-  typedef uint32_t ropev __attribute__((ext_vector_type(RPL / 4)));
+  static_assert(KVF == SAS_KV_NATIVE, "native rows only (fp8 rows run on attn3_kernel)");
   typedef MfmaOps<T> Ops;
 
   __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTG * STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) f32x4 xbuf[NW][4][64];  // partial Sᵀ of each wave
+  __shared__ __attribute__((aligned(16))) f32x4 xbuf[2][NW][4][64];  // partial Sᵀ of each wave, per tile of a pair
   __shared__ uint32_t rowid[RCH];
   __shared__ uint32_t tmask[RCH / TILE];
   __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
@@ -578,74 +577,20 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
         for (int j = 0; j < DMA_PER_TILE; ++j) dma_one(d, j);
       };
 
-      // ---- fp8 rows: VGPR loads, then dequantize into one ring stage ----
-      // wave w takes rows w + NW j (j < ROWS_PER_WAVE): lane l loads bytes 8l..8l+7
-      // (dims 8l..8l+7, scale l / 16) of each, and RPL rope bytes of row
-      // w + NW (l / (128 / RPL)).
-      struct Fp8Tile {
-        uint2 v[ROWS_PER_WAVE];
-        float s[ROWS_PER_WAVE];
-        ropev rope;
-      };
-      constexpr int ROPE_LPR = 128 / RPL;  // lanes per row for the rope bytes
-      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      auto fp8_load = [&](Fp8Tile& f, int tile) {
-        const uint64_t my_ptrs = (uint64_t)(uintptr_t)row_ptr(
-            rowid[tile * TILE + w + NW * (lane < ROWS_PER_WAVE ? lane : 0)]);
-        const char* rp = nullptr;
-#pragma unroll
-        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
-          const char* p = lane_row(my_ptrs, j);
-          const u32x2 t = __builtin_nontemporal_load((const SAS_GLOBAL u32x2*)(p + 8 * lane));
-          f.v[j] = make_uint2(t[0], t[1]);
-          f.s[j] = __builtin_nontemporal_load((const SAS_GLOBAL float*)(p + 512 + 4 * (lane >> 4)));
-          rp = (lane / ROPE_LPR == j) ? p : rp;
-        }
-        f.rope = __builtin_nontemporal_load(
-            (const SAS_GLOBAL ropev*)(rp + ROPE_OFF + (lane % ROPE_LPR) * RPL));
-      };
-      auto fp8_store = [&](const Fp8Tile& f, int tile) {
-        unsigned char* sb = kv_lds + (tile % NSTG) * STAGE_BYTES;
-#pragma unroll
-        for (int j = 0; j < ROWS_PER_WAVE; ++j) {
-          const int r = w + NW * j;
-          *(i16x8*)(sb + main_row_base(r) + 16 * lane) = fp8x8_dequant_bf16(f.v[j], f.s[j]);
-        }
-        // the lane's RPL rope bytes are whole 16-byte chunks; consecutive chunks of a
-        // row need not be adjacent in the rotated rope layout, so one store each
-        static_assert(RPL % 16 == 0, "rope bytes per lane");
-        const int r = w + NW * (lane / ROPE_LPR);
-        const int c0r = (lane % ROPE_LPR) * (RPL / 16);
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-        for (int k = 0; k < RPL / 16; ++k)
-          *(u32x4*)(sb + MAIN_BYTES + rope_slot(r, c0r + k) * 16) =
-              (u32x4){f.rope[4 * k], f.rope[4 * k + 1], f.rope[4 * k + 2], f.rope[4 * k + 3]};
-      };
-      Fp8Tile fpt;
-
-      if constexpr (FP8) {
-        Fp8Tile f1;
-        fp8_load(fpt, 0);
-        if (ntile > 1) fp8_load(f1, 1);
-        fp8_store(fpt, 0);
-        if (ntile > 1) fp8_store(f1, 1);
-      } else {
-        issue(0);
-        if (ntile > 1) issue(1);
-      }
+      // ---- prologue: tiles 0 and 1 into stages 0 and 1 (tile 1 reads the zero
+      // row when the chunk has a single tile: its rows are masked) ----
+      issue(0);
+      issue(1);
       // tile 0 has landed (tile 1's DMAs may be in flight; the query fragment and
       // the table words were waited for during the resolution)
-      if constexpr (!FP8) {
-        if (ntile > 1) wait_vmcnt<DMA_PER_TILE>(); else wait_vmcnt<0>();
-      }
+      wait_vmcnt<DMA_PER_TILE>();
       // the query fragment lives in AGPRs (the MFMAs read B operands from them
       // directly), leaving the VGPRs to the accumulators and prefetch buffers
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) asm volatile("" : "+a"(qf[ks]));
       __syncthreads();
 
-      // Addresses of the DMAs of tile t (t >= 2), gathered one iteration ahead.
+      // Addresses of the DMAs of tile t (t >= 2), gathered ahead of their issue.
       // Branch-free past the chunk's last tile: those instructions read the zero
       // row into the stage they would fill, which nothing reads before the chunk ends.
       auto next_addrs = [&](int tile) -> DmaAddrs {
@@ -659,87 +604,185 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
         }
         return d;
       };
-      DmaAddrs nd;
-      if constexpr (!FP8) nd = next_addrs(2);
       typedef const unsigned char SAS_LDS* lds_p;
-      for (int it = 0; it < ntile; ++it) {
-        // stage base as an LDS address, so every read below is one per-lane base
-        // plus an immediate offset
-        const lds_p sb = (lds_p)(kv_base + (uint32_t)((it % NSTG) * STAGE_BYTES));
-        // tile it + 2 into the stage tile it - 1 held (freed by barrier 2 of it - 1):
-        // fp8 rows are loaded here; native rows go out by DMA between the Q·Kᵀ MFMAs
-        // (their addresses were gathered during the previous iteration)
-        if constexpr (FP8) {
-          if (it + 2 < ntile) fp8_load(fpt, it + 2);
-        }
+      auto stage = [&](int tile) -> lds_p {
+        return (lds_p)(kv_base + (uint32_t)((tile % NSTG) * STAGE_BYTES));
+      };
 
-        // ---- partial Sᵀ of this tile over this wave's dims half ----
-        // K operands read KPF k-steps ahead (enough LDS reads in flight for one
-        // wave per SIMD to keep the LDS busy)
-        f32x16 st;
-        {
-          constexpr int KPF = SAS_KPF;
-          const lds_p kb = sb + qk_base;
-          auto kaddr = [&](int ks) -> const i16x8 SAS_LDS* {
-            return (const i16x8 SAS_LDS*)(ks < NKS_MAIN
-                                              ? kb + 32 * ks
-                                              : sb + (ks == NKS_MAIN ? rope_off0 : rope_off1));
-          };
-          i16x8 kbuf[KPF];
+      // ---- partial Sᵀ of one tile over this wave's dims half ----
+      // K operands read KPF k-steps ahead (enough LDS reads in flight for one wave
+      // per SIMD to keep the LDS busy); with DMA, the instructions of `dd` go out
+      // between the MFMAs (instruction j after MFMA j * NKS / DMA_PER_TILE)
+      auto qk_tile = [&](lds_p sb, const DmaAddrs& dd, auto with_dma, auto&& extra) -> f32x16 {
+        constexpr int KPF = SAS_KPF;
+        const lds_p kb = sb + qk_base;
+        auto kaddr = [&](int ks) -> const i16x8 SAS_LDS* {
+          return (const i16x8 SAS_LDS*)(ks < NKS_MAIN
+                                            ? kb + 32 * ks
+                                            : sb + (ks == NKS_MAIN ? rope_off0 : rope_off1));
+        };
+        i16x8 kbuf[KPF];
 #pragma unroll
-          for (int i = 0; i < KPF; ++i) kbuf[i] = *kaddr(i);
+        for (int i = 0; i < KPF; ++i) kbuf[i] = *kaddr(i);
+        // two accumulator chains (even / odd k-steps): an MFMA that reads the
+        // previous one's result waits for it to drain (about 58 instead of 32
+        // cycles per 32x32x16 MFMA, measured)
+        f32x16 s2[2];
 #pragma unroll
-          for (int j = 0; j < 16; ++j) st[j] = 0.0f;
-          // (scheduling fences keep each read KPF MFMAs ahead of its use; left
-          // alone, the scheduler sinks the reads next to their MFMAs)
+        for (int j = 0; j < 16; ++j) s2[0][j] = s2[1][j] = 0.0f;
+        // (scheduling fences keep each read KPF MFMAs ahead of its use; left
+        // alone, the scheduler sinks the reads next to their MFMAs)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const i16x8 kop = kbuf[ks % KPF];
+          if (ks + KPF < NKS) kbuf[ks % KPF] = *kaddr(ks + KPF);
+          s2[ks & 1] = Ops::mma(kop, qf[ks], s2[ks & 1]);
+          if (ks == 4) extra();  // VALU work of the caller, under the MFMAs
+          if constexpr (decltype(with_dma)::value) {
+#pragma unroll
+            for (int j = 0; j < DMA_PER_TILE; ++j)
+              if ((j * NKS) / DMA_PER_TILE == ks) dma_one(dd, j);
+          }
           __builtin_amdgcn_sched_barrier(0);
+        }
+        f32x16 st;
 #pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            const i16x8 kop = kbuf[ks % KPF];
-            if (ks + KPF < NKS) kbuf[ks % KPF] = *kaddr(ks + KPF);
-            st = Ops::mma(kop, qf[ks], st);
-            // DMA instruction j of tile it + 2 after MFMA j * NKS / DMA_PER_TILE
-            if constexpr (!FP8) {
+        for (int j = 0; j < 16; ++j) st[j] = s2[0][j] + s2[1][j];
+        return st;
+      };
+
+      // ---- Oᵀ (+)= Vᵀ·Pᵀ of one tile over both 16-row k-steps ----
+      // (Vᵀ operands read VPF MFMAs ahead; MFMA i = dv block i / 2, k-step i % 2;
+      // with the rescale, each accumulator block is multiplied just before its
+      // first MFMA; with DMA, instruction j of `dd` goes out after MFMA
+      // j * NPV / DMA_PER_TILE)
+      constexpr int VPF = SAS_VPF;
+      struct VBuf { i16x8 v[VPF]; };
+      // Vᵀ operand of MFMA i of a tile (spread order: all first k-steps, then all
+      // second ones)
+      auto vop = [&](lds_p sb, bool spread, int i) -> i16x8 {
+        const lds_p vb = sb + tr_base;
+        typedef i16x4 SAS_LDS* lds4;
+        const int d = spread ? i % DVB : i >> 1, kq = spread ? i / DVB : i & 1;
+        const i16x4 g0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds4)(vb + (16 * kq) * MAIN_ROW_BYTES + d * 64));
+        const i16x4 g1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds4)(vb + (16 * kq + 8) * MAIN_ROW_BYTES + 32 + d * 64));
+        return (i16x8){g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+      };
+      // the first VPF operands, read ahead of the tile's P·V (under other work)
+      auto pv_pre = [&](lds_p sb, auto rescale) -> VBuf {
+        constexpr bool SPREAD = SAS_PV_SPREAD || !decltype(rescale)::value;
+        VBuf vb;
 #pragma unroll
-              for (int j = 0; j < DMA_PER_TILE; ++j)
-                if ((j * NKS) / DMA_PER_TILE == ks) dma_one(nd, j);
+        for (int i = 0; i < VPF; ++i) vb.v[i] = vop(sb, SPREAD, i);
+        return vb;
+      };
+      auto pv_tile = [&](lds_p sb, VBuf vbf, const i16x8 (&pkt)[2], float alpha, const DmaAddrs& dd,
+                         auto rescale, auto with_dma) {
+        constexpr int NPV = 2 * DVB;
+        i16x8 (&vbuf)[VPF] = vbf.v;
+        // (no scheduling fences here: the compiler's own interleaving of the
+        // rescale multiplies with the MFMAs measured faster than fenced orders)
+        // MFMA order: with SAS_PV_SPREAD (or without the rescale) all first k-steps,
+        // then all second ones, so an accumulator's two MFMAs are DVB apart
+        constexpr bool SPREAD = SAS_PV_SPREAD || !decltype(rescale)::value;
+        auto vdk = [&](int i, int& d, int& kq) {
+          if (SPREAD) { d = i % DVB; kq = i / DVB; } else { d = i >> 1; kq = i & 1; }
+        };
+#pragma unroll
+        for (int i = 0; i < NPV; ++i) {
+          int d, kq;
+          vdk(i, d, kq);
+          if constexpr (decltype(rescale)::value) {
+            if (kq == 0) {
+#pragma unroll
+              for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
             }
-            __builtin_amdgcn_sched_barrier(0);
+          }
+          const i16x8 aop = vbuf[i % VPF];
+          if (i + VPF < NPV) vbuf[i % VPF] = vop(sb, SPREAD, i + VPF);
+          acc[d] = Ops::mma(aop, pkt[kq], acc[d]);
+          if constexpr (decltype(with_dma)::value) {
+#pragma unroll
+            for (int j = 0; j < DMA_PER_TILE; ++j)
+              if ((j * NPV) / DMA_PER_TILE == i) dma_one(dd, j);
           }
         }
+      };
+
+      // Two tiles (64 rows) per softmax step, so the accumulator rescale and the
+      // running-max bookkeeping are paid once per 64 rows (golden.py:187-191's
+      // rule at 64-row tiles). Pair p = tiles a = 2p, b = 2p + 1 of the chunk (a
+      // trailing odd tile pairs with a masked zero-row tile); the 3-stage ring
+      // holds a, b and tile a + 2:
+      //   Q·Kᵀ(a), DMAs of tile a + 2 between its MFMAs (into the stage tile
+      //     a - 1 left); partial of a to LDS; wait for this wave's DMAs of b;
+      //   barrier 1a (b in LDS);  Q·Kᵀ(b); partial of b to LDS;
+      //   barrier 1b (both partials written);  softmax over the 64 rows;
+      //   P·V(a) with the rescale;  barrier X (stage a free);
+      //   P·V(b), DMAs of tile a + 3 between its MFMAs (into stage a);
+      //   wait for this wave's DMAs of a + 2;  barrier 2 (stage b free, a + 2 in LDS).
+      const int npair = (ntile + 1) >> 1;
+      DmaAddrs nd = next_addrs(2);
+      for (int pp = 0; pp < npair; ++pp) {
+        const int ta = 2 * pp;
+        const lds_p sa = stage(ta);
+        const lds_p sbt = stage(ta + 1);
+
+        const f32x16 st0 = qk_tile(sa, nd, std::true_type{}, [] {});
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          xbuf[w][j][lane] = (f32x4){st[4 * j], st[4 * j + 1], st[4 * j + 2], st[4 * j + 3]};
-        const uint32_t vm = tmask[it] >> (4 * hl);
-        __syncthreads();  // barrier 1: both partials of every head group are written
-        DmaAddrs nd3;
-        if constexpr (!FP8) nd3 = next_addrs(it + 3);  // (rowid reads under the softmax)
-
-        // ---- full Sᵀ = own + partner's (the same float sums on both waves) ----
-        float sv[16];
-        {
-          f32x4 o[4];
+          xbuf[0][w][j][lane] = (f32x4){st0[4 * j], st0[4 * j + 1], st0[4 * j + 2], st0[4 * j + 3]};
+        wait_vmcnt<DMA_PER_TILE>();  // this wave's share of tile b (a + 2's may be in flight)
+        __syncthreads();             // barrier 1a: tile b in LDS, partials of a written
+        // ---- full Sᵀ = own + partner's (the same float sums on both waves); tile
+        // a's sums are formed under the Q·Kᵀ MFMAs of tile b ----
+        float sv[32];
+        f32x4 oa[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) o[j] = xbuf[partner][j][lane];
+        for (int j = 0; j < 4; ++j) oa[j] = xbuf[0][partner][j][lane];
+        const f32x16 st1 = qk_tile(sbt, nd, std::false_type{}, [&] {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sv[4 * j + e] = st[4 * j + e] + o[j][e];
+            for (int e = 0; e < 4; ++e) sv[4 * j + e] = st0[4 * j + e] + oa[j][e];
+        });
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xbuf[1][w][j][lane] = (f32x4){st1[4 * j], st1[4 * j + 1], st1[4 * j + 2], st1[4 * j + 3]};
+        const uint32_t tm0 = tmask[ta], tm1 = tmask[ta + 1];
+        __syncthreads();  // barrier 1b: the partials of b are written
+        const DmaAddrs nd3 = next_addrs(ta + 3);  // (rowid reads under the softmax)
+        VBuf vba = pv_pre(sa, std::true_type{});   // (Vᵀ reads of P·V(a) under the softmax)
+        {
+          f32x4 o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = xbuf[1][partner][j][lane];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sv[16 + 4 * j + e] = st1[4 * j + e] + o[j][e];
         }
-        // ---- online softmax (exp2 domain) on rows 8(i/4) + 4hl + i%4 ----
+        // ---- online softmax (exp2 domain) on rows 8(i/4) + 4hl + i%4 of each tile ----
         // (masking only on tiles with invalid rows: tile tails, -1 / out-of-range ids;
         // the empty asm keeps this a branch, so full tiles skip the selects)
-        if (__builtin_amdgcn_readfirstlane(tmask[it]) != 0xFFFFFFFFu) {
+        if (__builtin_amdgcn_readfirstlane(tm0 & tm1) != 0xFFFFFFFFu) {
           asm volatile("");
+          const uint32_t vm0 = tm0 >> (4 * hl), vm1 = tm1 >> (4 * hl);
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            sv[i] = ((vm >> (8 * (i / 4) + (i % 4))) & 1u) ? sv[i] : -INFINITY;
+          for (int i = 0; i < 16; ++i) {
+            const int bit = 8 * (i / 4) + (i % 4);
+            sv[i] = ((vm0 >> bit) & 1u) ? sv[i] : -INFINITY;
+            sv[16 + i] = ((vm1 >> bit) & 1u) ? sv[16 + i] : -INFINITY;
+          }
         }
         // max of the raw scores, then scaled: rounding is monotonic, so this is
         // the max of the scaled scores
         float mloc = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, sv[i]);
+        for (int i = 0; i < 32; ++i) mloc = fmaxf(mloc, sv[i]);
         mloc = wave_max_pair(mloc) * sc;
         const bool grow = mloc > m_run;
         const float m_new = grow ? mloc : m_run;
@@ -749,70 +792,38 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
         // a head with no key and no sink yet (m_run = -inf) has every score -inf:
         // subtracting 0 instead keeps its P at exactly 0
         const float m_sub = m_run == -INFINITY ? 0.0f : m_run;
-        i16x8 pk[2];
+        i16x8 pk0[2], pk1[2];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], sc, -m_sub));
           l_part += p;
-          pk[i / 8][i % 8] = Ops::from_f32(p);
+          pk0[i / 8][i % 8] = Ops::from_f32(p);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[16 + i], sc, -m_sub));
+          l_part += p;
+          pk1[i / 8][i % 8] = Ops::from_f32(p);
         }
 
-        // ---- Oᵀ = alpha·Oᵀ + Vᵀ·Pᵀ over both 16-row k-steps ----
-        // (Vᵀ operands read VPF MFMAs ahead; MFMA i = dv block i / 2, k-step i % 2.
-        // Multiplying every tile costs less than branching on whether any head's
-        // max moved: the two paths would hold the accumulators in different registers)
-        auto pv_tile = [&](auto rescale) {
-          constexpr int VPF = SAS_VPF;
-          constexpr int NPV = 2 * DVB;
-          const lds_p vb = sb + tr_base;
-          typedef i16x4 SAS_LDS* lds4;
-          auto vop = [&](int i) -> i16x8 {
-            const int d = i >> 1, kq = i & 1;
-            const i16x4 g0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds4)(vb + (16 * kq) * MAIN_ROW_BYTES + d * 64));
-            const i16x4 g1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds4)(vb + (16 * kq + 8) * MAIN_ROW_BYTES + 32 + d * 64));
-            return (i16x8){g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
-          };
-          i16x8 vbuf[VPF];
-#pragma unroll
-          for (int i = 0; i < VPF; ++i) vbuf[i] = vop(i);
-          // (no scheduling fences here: the compiler's own interleaving of the
-          // rescale multiplies with the MFMAs measured faster than fenced orders)
-#pragma unroll
-          for (int i = 0; i < NPV; ++i) {
-            const int d = i >> 1, kq = i & 1;
-            if constexpr (decltype(rescale)::value) {
-              if (kq == 0) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) acc[d][j] *= alpha;
-              }
-            }
-            const i16x8 aop = vbuf[i % VPF];
-            if (i + VPF < NPV) vbuf[i % VPF] = vop(i + VPF);
-            acc[d] = Ops::mma(aop, pk[kq], acc[d]);
-          }
-        };
-        pv_tile(std::true_type{});
-
-        if constexpr (FP8) {
-          // tile it + 2 into its stage (tile it - 1's, free since barrier 2 of it - 1)
-          if (it + 2 < ntile) fp8_store(fpt, it + 2);
-        } else {
-          // this wave's share of tile it + 1 has landed (tile it + 2's may be in flight)
-          wait_vmcnt<DMA_PER_TILE>();
-        }
-        __syncthreads();  // barrier 2: stage and partials free; tile it + 1 in LDS
-        if constexpr (!FP8) nd = nd3;
+        pv_tile(sa, vba, pk0, alpha, nd3, std::true_type{}, std::false_type{});
+        VBuf vbb = pv_pre(sbt, std::false_type{});  // (read while the barrier waits)
+        __syncthreads();  // barrier X: stage a is free
+        pv_tile(sbt, vbb, pk1, alpha, nd3, std::false_type{}, std::true_type{});
+        nd = next_addrs(ta + 4);
+        wait_vmcnt<DMA_PER_TILE>();  // this wave's share of tile a + 2 (a + 3's in flight)
+        __syncthreads();             // barrier 2: stage b free; tile a + 2 in LDS
       }
-      if constexpr (!FP8) wait_vmcnt<0>();  // the last (zero-row) DMAs have landed
+      wait_vmcnt<0>();  // the last (zero-row) DMAs have landed
     }
 
     // ---- row sums of the two row halves (lanes l and l ^ 32, same head) ----
     const float l_run = wave_sum_pair(l_part);
 
-    // ---- epilogue: the item's rows go out through LDS (the ring is free), so
-    // every store instruction writes whole rows ----
+    // ---- epilogue: the item's rows go out through LDS (the ring is free once
+    // every wave's last DMAs have landed), so every store instruction writes
+    // whole rows ----
+    __syncthreads();
     {
       unsigned char* stg = kv_lds;
       const int nh = min(MB, a.num_heads - hb * MB);  // heads of this item
@@ -1836,12 +1847,17 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     const int per_xcd = (a.num_fa + 7) / 8;
     // native rows: one wave per SIMD (attn2_kernel); fp8 rows: the pipelined
     // two-waves-per-SIMD kernel, whose second wave hides the dequantization
-    if (KVF == SAS_KV_FP8_DS_MLA || (a.phases & SAS_PHASE_PIPELINED))
+    if constexpr (KVF == SAS_KV_FP8_DS_MLA) {
       hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
                          dim3(256 * NHG), 0, st, a);
-    else
-      hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
-                         dim3(128 * NHG), 0, st, a);
+    } else {
+      if (a.phases & SAS_PHASE_PIPELINED)
+        hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
+                           dim3(256 * NHG), 0, st, a);
+      else
+        hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
+                           dim3(128 * NHG), 0, st, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

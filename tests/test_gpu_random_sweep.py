@@ -13,15 +13,16 @@ an output by up to ~2e-2.
 
 Asserted for every case (the accuracy contract):
 * against golden, the bound that golden's own algorithm meets when it walks
-  the attended rows in the kernel's 32-row tiles: at least 99.25 % of the
-  elements within the reference's rule (rtol 2^-7, atol 1e-4;
+  the attended rows in the kernel's 32- or 64-row steps: at least 99.25 % of
+  the elements within the reference's rule (rtol 2^-7, atol 1e-4;
   test_sparse_attn_sharedkv.py:394-481) and at most one element beyond
   atol = rtol = 2e-2. Over the 300 configurations of ``oracle.rescale_study``
   golden at 32-row tiles has at least 99.308 % within the rule (3 cases under
-  the reference's 99.5 %) and no element beyond 2e-2; the kernel's order of
-  rounding (eager running max per 32-row tile) 99.304 % and one element beyond
-  2e-2 in one case. The reference's 99.5 % holds for golden's own 512-row tiles
-  only, so it is reported here, not asserted;
+  the reference's 99.5 %) and golden at 64-row tiles at least 99.296 % (2
+  cases under), neither with an element beyond 2e-2; the kernel's order of
+  rounding (eager running max per 64-row softmax step) at least 99.296 % and
+  one element beyond 2e-2 in two cases. The reference's 99.5 % holds for
+  golden's own 512-row tiles only, so it is reported here, not asserted;
 * the LSE within 1e-3 relative of golden;
 * the output as accurate as golden against the float64 closed form (max
   |out - exact| <= 2 max |golden - exact| + 2^-9 max |exact|).
@@ -47,7 +48,7 @@ requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
 if HAS_GPU:
     from sparse_attn_sharedkv_amd import sparse_attn_sharedkv, sparse_attn_sharedkv_metadata
 
-# the bound golden's own algorithm meets at the kernel's 32-row tiles (module docstring)
+# the bound golden's own algorithm meets at the kernel's step sizes (module docstring)
 MIN_PCT_REF_RULE = 99.25
 MAX_BEYOND_2E2 = 1
 
