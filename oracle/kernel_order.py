@@ -34,12 +34,15 @@ LN2 = 0.6931471805599453
 def attend_token_kernel_order(q: torch.Tensor, segments: Sequence[torch.Tensor],
                               sinks: torch.Tensor, softmax_scale: float, *,
                               d_v: Optional[int] = None, tile: int = 32, tau: float = 8.0,
-                              streams: int = 1, segment_tiles: bool = False
+                              streams: int = 1, segment_tiles: bool = False,
+                              out_dtype: Optional[torch.dtype] = None
                               ) -> Tuple[torch.Tensor, torch.Tensor]:
     """One query token's ``(out [G, d_v], lse [G])`` in the kernel's rounding order.
 
     ``segment_tiles``: cut each segment into tiles on its own (golden's order)
-    instead of tiling the concatenated list (the kernel's order).
+    instead of tiling the concatenated list (the kernel's order). ``out_dtype``:
+    the type ``acc / l`` is rounded to (default: the input type; float32 for a
+    split piece's partial).
     """
     dtype = q.dtype
     g, d = q.shape
@@ -87,9 +90,49 @@ def attend_token_kernel_order(q: torch.Tensor, segments: Sequence[torch.Tensor],
         w = torch.where(torch.isnan(w), torch.zeros_like(w), w)
         lt = lt + w * l[i]
         at = at + w[:, None] * acc[i]
-    out = (at / lt[:, None]).to(dtype)
+    out = (at / lt[:, None]).to(dtype if out_dtype is None else out_dtype)
     lse = (mt + torch.log2(lt)) * torch.tensor(LN2, dtype=torch.float32)
     return out, lse
+
+
+def attend_token_split(q: torch.Tensor, segments: Sequence[torch.Tensor], sinks: torch.Tensor,
+                       softmax_scale: float, *, d_v: Optional[int] = None, tile: int = 64,
+                       pieces: int = 2, partial_dtype: torch.dtype = torch.float32
+                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One token split into ``pieces`` contiguous pieces of the attended list (cut at
+    multiples of ``tile``), each in the kernel's order without the sink, its
+    partial ``acc / l`` rounded to ``partial_dtype``, merged in fp32 as the merge
+    kernel does: lse = m + ln(e^(sink - m) + sum_i e^(lse_i - m)) over
+    m = max(sink, lse_i), out = RNE(sum_i e^(lse_i - lse) o_i)."""
+    dtype = q.dtype
+    g = q.shape[0]
+    dv = q.shape[1] if d_v is None else int(d_v)
+    segs = [s for s in segments if s.shape[0] > 0]
+    rows = torch.cat(segs) if segs else torch.zeros((0, q.shape[1]), dtype=dtype)
+    n = rows.shape[0]
+    cuts = [0] + [min(n, -(-(n * k // pieces) // tile) * tile) for k in range(1, pieces)] + [n]
+    no_sink = torch.full((g,), -math.inf, dtype=torch.float32)
+    parts = []
+    for lo, hi in zip(cuts, cuts[1:]):
+        if hi > lo:
+            parts.append(attend_token_kernel_order(q, [rows[lo:hi]], no_sink, softmax_scale, d_v=dv,
+                                                   tile=tile, tau=0.0, out_dtype=partial_dtype))
+    sink = sinks.to(torch.float32)
+    mx = sink.clone()
+    for _, l in parts:
+        mx = torch.maximum(mx, l)
+    tot = torch.where(torch.isfinite(mx), torch.exp(sink - mx), torch.zeros_like(mx))
+    tot = torch.where(torch.isnan(tot), torch.zeros_like(tot), tot)
+    for _, l in parts:
+        e = torch.exp(l - mx)
+        tot = tot + torch.where(torch.isnan(e), torch.zeros_like(e), e)
+    lse = mx + torch.log(tot)
+    out = torch.zeros((g, dv), dtype=torch.float32)
+    for o, l in parts:
+        w = torch.exp(l - lse)
+        w = torch.where(torch.isnan(w), torch.zeros_like(w), w)
+        out = out + w[:, None] * o.to(torch.float32)
+    return out.to(dtype), lse
 
 
 def sparse_attn_kernel_order(q: torch.Tensor, *, tile: int = 32, tau: float = 8.0,

@@ -6,8 +6,7 @@ For each random configuration of the GPU sweep (``gen.random_sweep_cfg``, the
 reference's U(-10, 10) inputs) it computes golden (``golden_ref``, 512-row
 tiles), the float64 closed form, golden with 32- and 64-row tiles, and the
 kernel's order (``kernel_order``) for several step sizes, thresholds ``tau``
-and stream counts, and
-reports per variant how many configurations fail the reference's rule
+and stream counts, split-KV pieces (fp32 / bf16 partials), and reports per variant how many configurations fail the reference's rule
 (>= 99.5 % of elements within rtol 2^-7 / atol 1e-4 of golden) and how many
 have elements beyond atol = rtol = 2e-2 of golden.
 
@@ -27,13 +26,19 @@ import torch
 
 from . import gen
 from .golden_ref import attend_token, sparse_attn_exact, sparse_attn_oracle
-from .kernel_order import compare, sparse_attn_kernel_order
+from .kernel_order import attend_token_split, compare, sparse_attn_kernel_order
 
 # (name, tile, tau, streams); "golden32" / "golden64" are golden's own algorithm at
 # 32- / 64-row tiles; "t64_tau0" is the kernel's order (64-row softmax steps, eager max)
 VARIANTS = [("golden32", 32, None, 1), ("golden64", 64, None, 1), ("t64_tau0", 64, 0.0, 1),
             ("t64_tau8", 64, 8.0, 1)] + [(f"tau{t}", 32, float(t), 1) for t in (0, 1, 2, 4, 8)] + \
            [("tau0_s2", 32, 0.0, 2), ("tau8_s2", 32, 8.0, 2)]
+
+
+# split-KV variants: every token's attended list cut into two pieces at a 64-row
+# boundary (each piece golden's own rule at 64-row tiles, without the sink),
+# partials in fp32 or bf16, merged as the merge kernel does
+SPLITS = [("t64_split2_f32", torch.float32), ("t64_split2_bf16", torch.bfloat16)]
 
 
 def run_case(i: int) -> dict:
@@ -52,12 +57,17 @@ def run_case(i: int) -> dict:
         else:
             x, _ = sparse_attn_kernel_order(tile=tile, tau=tau, streams=streams, **kw)
         res[name] = compare(x, ref, ex)
+    for name, pd in SPLITS:
+        def split(qt, segments, sinks, scale, d_v=None, pd=pd):
+            return attend_token_split(qt, segments, sinks, scale, d_v=d_v, tile=64, pieces=2,
+                                      partial_dtype=pd)
+        res[name] = compare(sparse_attn_oracle(attend=split, **kw)[0], ref, ex)
     return res
 
 
 def summarize(rows: list) -> dict:
     out = {}
-    for name, *_ in VARIANTS:
+    for name in [v[0] for v in VARIANTS] + [x[0] for x in SPLITS]:
         v = [r[name] for r in rows]
         pct = np.array([x["pct_ref"] for x in v])
         beyond = np.array([x["beyond_2e2"] for x in v])

@@ -103,3 +103,30 @@ def test_streams_and_tile_size_change_rounding_not_math():
         assert (o.float() - o3.float()).abs().max() <= 2e-2
     for l in (l1, l2, l4):
         assert torch.allclose(l, l3, rtol=1e-5)
+
+
+def test_split_pieces_merge_like_the_closed_form():
+    # a token split into two pieces (each without the sink, partials in fp32) and
+    # merged in fp32 equals the closed-form merge of the same pieces, and one
+    # piece is the unsplit kernel order
+    from oracle.golden_ref import merge_partials
+    from oracle.kernel_order import attend_token_split
+    g = torch.Generator().manual_seed(7)
+    q = (torch.randn(32, 576, generator=g) * 2).to(torch.bfloat16)
+    rows = (torch.randn(700, 576, generator=g) * 2).to(torch.bfloat16)
+    sinks = torch.randn(32, generator=g)
+    scale = 1 / math.sqrt(576)
+    o1, l1 = attend_token_split(q, [rows], sinks, scale, d_v=512, pieces=1)
+    ow, lw = attend_token_kernel_order(q, [rows], sinks, scale, d_v=512, tile=64, tau=0.0)
+    assert torch.equal(o1, ow) and torch.allclose(l1, lw, rtol=1e-6, atol=1e-6)
+    o2, l2 = attend_token_split(q, [rows], sinks, scale, d_v=512, pieces=2)
+    no_sink = torch.full((32,), -math.inf)
+    pa = attend_token_kernel_order(q, [rows[:384]], no_sink, scale, d_v=512, tile=64, tau=0.0,
+                                   out_dtype=torch.float32)
+    pb = attend_token_kernel_order(q, [rows[384:]], no_sink, scale, d_v=512, tile=64, tau=0.0,
+                                   out_dtype=torch.float32)
+    om, lm = merge_partials([pa[0].numpy(), pb[0].numpy()], [pa[1].numpy(), pb[1].numpy()],
+                            sinks.numpy())
+    d = (o2.float() - torch.from_numpy(om).float()).abs()
+    assert (d <= torch.finfo(torch.bfloat16).eps * torch.from_numpy(np.abs(om)).float() + 1e-6).all()
+    assert np.allclose(l2.numpy(), lm, rtol=1e-5, atol=1e-5)
