@@ -317,6 +317,17 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   const char* ori_kv = (const char*)a.ori_kv;
   const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
   const float sc = a.softmax_scale * LOG2E;
+  // With at most 64 batches, every batch's lengths and query offset sit in one
+  // lane each, loaded at the start beside the metadata row (they no longer wait
+  // for it: the item's batch picks its lane).
+  const bool lens_in_lanes = a.batch <= 64;
+  int lane_aq = 0, lane_kv = 0, lane_qp = 0;
+  if (lens_in_lanes) {
+    const int lb = lane < a.batch ? lane : a.batch - 1;
+    lane_aq = a.act_q_lens[lb];
+    lane_kv = a.seqused_kv[lb];
+    lane_qp = a.q_prefix[lb];
+  }
   if (tid < 2) first_neg[tid] = INT32_MAX;
   __syncthreads();
 
@@ -337,9 +348,15 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
     int act_q, act_kv, qpre;
     auto load_batch = [&] {
       const int bc = b < a.batch ? b : a.batch - 1;
-      act_q = ld_uniform(a.act_q_lens + bc);
-      act_kv = ld_uniform(a.seqused_kv + bc);
-      qpre = ld_uniform(a.q_prefix + bc);
+      if (lens_in_lanes) {
+        act_q = __builtin_amdgcn_readlane(lane_aq, bc);
+        act_kv = __builtin_amdgcn_readlane(lane_kv, bc);
+        qpre = __builtin_amdgcn_readlane(lane_qp, bc);
+      } else {
+        act_q = ld_uniform(a.act_q_lens + bc);
+        act_kv = ld_uniform(a.seqused_kv + bc);
+        qpre = ld_uniform(a.q_prefix + bc);
+      }
     };
     load_batch();
     // normalise the cursor: skip batches with no (more) query rows
