@@ -1361,7 +1361,10 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       // ---- fp8 rows: VGPR loads, then dequantize into one ring stage ----
       // wave w takes rows w + NW j (j < ROWS_PER_WAVE): lane l loads bytes 8l..8l+7
       // (dims 8l..8l+7, scale l / 16) of each, and RPL rope bytes of row
-      // w + NW (l / (128 / RPL)).
+      // w + NW (l / (128 / RPL)). Ordinary (L2-allocating) loads: the token's other
+      // 64-head m-block reads the same rows on the same XCD shortly after, and
+      // finds them in L2 (measured: 9 % fewer HBM bytes than streaming loads, at
+      // +0.5 % kernel time).
       struct Fp8Tile {
         uint2 v[ROWS_PER_WAVE];
         float s[ROWS_PER_WAVE];
@@ -1376,12 +1379,12 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
 #pragma unroll
         for (int j = 0; j < ROWS_PER_WAVE; ++j) {
           const char* p = lane_row(my_ptrs, j);
-          const u32x2 t = __builtin_nontemporal_load((const SAS_GLOBAL u32x2*)(p + 8 * lane));
+          const u32x2 t = *((const SAS_GLOBAL u32x2*)(p + 8 * lane));
           f.v[j] = make_uint2(t[0], t[1]);
-          f.s[j] = __builtin_nontemporal_load((const SAS_GLOBAL float*)(p + 512 + 4 * (lane >> 4)));
+          f.s[j] = *((const SAS_GLOBAL float*)(p + 512 + 4 * (lane >> 4)));
           rp = (lane / ROPE_LPR == j) ? p : rp;
         }
-        f.rope = __builtin_nontemporal_load(
+        f.rope = *(
             (const SAS_GLOBAL ropev*)(rp + ROPE_OFF + (lane % ROPE_LPR) * RPL));
       };
       auto fp8_store = [&](const Fp8Tile& f, int tile) {
