@@ -1087,19 +1087,30 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
 
   // Sinks of this lane's softmax head in the (at most two) head blocks of an
   // item, loaded once: a load per item would also wait for the previous item's
-  // output stores (one in-order counter covers loads and stores).
+  // output stores (one in-order counter covers loads and stores). They are
+  // first read after the first item's resolution has waited for its loads.
   const float sink_hb0 = hq < a.num_heads ? a.sinks[hq] : -INFINITY;
   const float sink_hb1 = MB + hq < a.num_heads ? a.sinks[MB + hq] : -INFINITY;
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
   int item_par = 0;  // which first_neg slot the next top-k scan uses
   bool first_item = true;
   for (;;) {
     b = __builtin_amdgcn_readfirstlane(b);
     m = __builtin_amdgcn_readfirstlane(m);
+    // the batch's lengths and query offset, loaded together (one scalar round
+    // trip; the index is clamped, so past the last batch they are not used)
+    int act_q, act_kv, qpre;
+    auto load_batch = [&] {
+      const int bc = b < a.batch ? b : a.batch - 1;
+      act_q = ld_uniform(a.act_q_lens + bc);
+      act_kv = ld_uniform(a.seqused_kv + bc);
+      qpre = ld_uniform(a.q_prefix + bc);
+    };
+    load_batch();
     // normalise the cursor: skip batches with no (more) query rows
-    while (b < a.batch && b <= b_end && m >= ld_uniform(a.act_q_lens + b) * hblocks) {
+    while (b < a.batch && b <= b_end && m >= act_q * hblocks) {
       ++b;
       m = 0;
+      load_batch();
     }
     if (b >= a.batch || b > b_end || (b == b_end && m > s_end)) break;
     const bool is_end = (b == b_end && m == s_end);
@@ -1107,9 +1118,7 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
     const int hb = m - s * hblocks;
     if (is_end && j_end == 0) break;
 
-    const int act_q = ld_uniform(a.act_q_lens + b);
-    const int act_kv = ld_uniform(a.seqused_kv + b);
-    const int tok = ld_uniform(a.q_prefix + b) + s;
+    const int tok = qpre + s;
     const ItemGeom g =
         item_geom(act_q, act_kv, s, a.ori_win_left, a.scenario, a.cmp_ratio, a.topk);
     const int L = g.n_win + g.n_cmp;
@@ -1127,9 +1136,13 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
     // ---- online-softmax state of head hq (golden.py:156-160 seeds m = sink,
     // l = 1; the 1 goes to the lanes of group 0 of the first row half, whose row
     // sums are added to the others' at the end) ----
-    const float sink_v = hb == 0 ? sink_hb0 : sink_hb1;
     const bool hq_ok = hb * MB + hq < a.num_heads;
-    float m_run = partial ? -INFINITY : (hq_ok ? sink_v * LOG2E : -INFINITY);
+    // the sink seeds m_run once the item's first loads have been waited for
+    auto seed_m = [&]() -> float {
+      const float sink_v = hb == 0 ? sink_hb0 : sink_hb1;
+      return partial ? -INFINITY : (hq_ok ? sink_v * LOG2E : -INFINITY);
+    };
+    float m_run = -INFINITY;
     float l_part = (partial || g4 != 0 || rh != 0) ? 0.0f : 1.0f;
     float mx = -INFINITY;
     f32x16 acc[DVB];
@@ -1267,6 +1280,7 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       }
       // every load so far (table words, query fragment) has landed, as the compiler sees it
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+      if (c0 == p_lo) m_run = seed_m();
       if (stop_pending) {
         __syncthreads();  // every thread's atomicMin is in
         cmp_stop = min(first_neg[item_par], g.n_cmp);
@@ -1619,6 +1633,7 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       }
     }
 
+    if (p_lo >= p_hi) m_run = seed_m();  // an item with no rows: the sink alone
     // ---- row sums of head hq over the wave's four lanes and both row halves;
     // (m, l) to the P·V layout (head hp = hg * 32 + lane % 32) ----
     {
