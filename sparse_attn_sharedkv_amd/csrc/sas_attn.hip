@@ -240,7 +240,11 @@ __device__ inline i16x8 fp8x8_dequant_bf16(uint2 v, float s) {
 // free, a + 2 landed). Ring of 3 stages: tile a + 2 is issued under the Q·Kᵀ
 // of a into the stage tile a - 1 left, a + 3 under the P·V of b into stage a.
 // Native rows only: fp8 rows run on attn3_kernel.
-template <int DQK, int DV, int NHG, typename T, int KVF>
+// PREF: launches whose batches hold several query rows (prefill, MTP); then a
+// workgroup's consecutive items of one batch load the next item's query
+// fragment during the current item's epilogue. Decode launches keep the
+// simpler first-chunk load (measured faster for their short items).
+template <int DQK, int DV, int NHG, typename T, int KVF, bool PREF>
 __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   constexpr int NW = 2 * NHG;            // waves per workgroup
   constexpr int MB = 32 * NHG;           // heads per item (m-block)
@@ -340,30 +344,49 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   const float sink_hb1 = MB + hlocal < a.num_heads ? a.sinks[MB + hlocal] : -INFINITY;
   int item_par = 0;  // which first_neg slot the next top-k scan uses
   bool first_item = true;
+  // query fragment of this wave's dims half (B operand of Sᵀ = K·Qᵀ); the next
+  // item's is loaded into it during the current item's last step (q_pref)
+  i16x8 qf[NKS];
+  bool q_pref = false;
+  // a batch's lengths and query offset: from the lanes (at most 64 batches) or
+  // by scalar loads, issued together (the index is clamped)
+  auto batch_lens = [&](int bb, int& aq, int& akv, int& qp) {
+    const int bc = bb < a.batch ? bb : a.batch - 1;
+    if (lens_in_lanes) {
+      aq = __builtin_amdgcn_readlane(lane_aq, bc);
+      akv = __builtin_amdgcn_readlane(lane_kv, bc);
+      qp = __builtin_amdgcn_readlane(lane_qp, bc);
+    } else {
+      aq = ld_uniform(a.act_q_lens + bc);
+      akv = ld_uniform(a.seqused_kv + bc);
+      qp = ld_uniform(a.q_prefix + bc);
+    }
+  };
+  // this wave's query fragment of (token, head), zero for rows out of range
+  auto load_q = [&](int qtok, int qhead) {
+    const bool ok = qtok >= 0 && qtok < a.total_tokens && qhead < a.num_heads;
+    const short* qrow = (const short*)a.q + ((size_t)(ok ? qtok : 0) * a.num_heads +
+                                             (ok ? qhead : 0)) * DQK;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int dim = ks < NKS_MAIN ? (256 * dh + 16 * ks + 8 * hl)
+                                    : (512 + 32 * dh + 16 * (ks - NKS_MAIN) + 8 * hl);
+      i16x8 v = *(const i16x8*)(qrow + dim);
+      qf[ks] = ok ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  };
   for (;;) {
+    const bool have_q = PREF && q_pref;
+    q_pref = false;
     b = __builtin_amdgcn_readfirstlane(b);
     m = __builtin_amdgcn_readfirstlane(m);
-    // the batch's lengths and query offset, loaded together (one scalar round
-    // trip; the index is clamped, so past the last batch they are not used)
     int act_q, act_kv, qpre;
-    auto load_batch = [&] {
-      const int bc = b < a.batch ? b : a.batch - 1;
-      if (lens_in_lanes) {
-        act_q = __builtin_amdgcn_readlane(lane_aq, bc);
-        act_kv = __builtin_amdgcn_readlane(lane_kv, bc);
-        qpre = __builtin_amdgcn_readlane(lane_qp, bc);
-      } else {
-        act_q = ld_uniform(a.act_q_lens + bc);
-        act_kv = ld_uniform(a.seqused_kv + bc);
-        qpre = ld_uniform(a.q_prefix + bc);
-      }
-    };
-    load_batch();
+    batch_lens(b, act_q, act_kv, qpre);
     // normalise the cursor: skip batches with no (more) query rows
     while (b < a.batch && b <= b_end && m >= act_q * hblocks) {
       ++b;
       m = 0;
-      load_batch();
+      batch_lens(b, act_q, act_kv, qpre);
     }
     if (b >= a.batch || b > b_end || (b == b_end && m > s_end)) break;
     const bool is_end = (b == b_end && m == s_end);
@@ -385,12 +408,32 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
     const int p_hi = bhi * s2b < L ? bhi * s2b : L;
     const bool tok_ok = tok >= 0 && tok < a.total_tokens;
 
-    // query fragment for this wave's dims half (B operand of Sᵀ = K·Qᵀ)
-    i16x8 qf[NKS];
     // ---- online-softmax state (golden.py:156-160 seeds m = sink, l = 1; the 1
     // goes to the lanes of the lower row half, whose row sums are added to the
     // upper half's at the end) ----
     const int hb = m - s * hblocks;
+    // the next item of this workgroup, if it is the next query row or head block
+    // of the same batch: its query fragment is loaded into qf once this item's
+    // last Q·Kᵀ has read qf
+    auto prefetch_next_q = [&]() -> bool {
+      if (is_end) return false;
+      int nb = b, nm = m + 1, aq, akv, qp;
+      batch_lens(nb, aq, akv, qp);
+      while (nb < a.batch && nb <= b_end && nm >= aq * hblocks) {
+        ++nb;
+        nm = 0;
+        batch_lens(nb, aq, akv, qp);
+      }
+      if (nb >= a.batch || nb > b_end || (nb == b_end && nm > s_end)) return false;
+      if (nb == b_end && nm == s_end && j_end == 0) return false;
+      // only within a batch (prefill-like runs of query rows): for decode items of
+      // other batches the early loads delayed this item's output stores by more
+      // than they saved (SWA decode +4 %, A/B)
+      if (nb != b) return false;
+      const int ns = nm / hblocks;
+      load_q(qp + ns, (nm - ns * hblocks) * MB + hlocal);
+      return true;
+    };
     // the sink seeds m_run once the item's first loads have been waited for
     auto seed_m = [&]() -> float {
       const float sink_v = hb == 0 ? sink_hb0 : sink_hb1;
@@ -421,20 +464,11 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
     for (int c0 = p_lo; c0 < p_hi; c0 += RCH) {
       const int clen = (p_hi - c0) < RCH ? (p_hi - c0) : RCH;
       const int ntile = (clen + TILE - 1) / TILE;
-      // query fragment of the item (first chunk): compiler-visible loads issued
-      // before the resolution's loads, so they land during its memory round
-      // trips; the compiler's wait for the table words below covers them
-      if (c0 == p_lo) {
-        const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
-                                                 (head_ok ? head : 0)) * DQK;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const int dim = ks < NKS_MAIN ? (256 * dh + 16 * ks + 8 * hl)
-                                        : (512 + 32 * dh + 16 * (ks - NKS_MAIN) + 8 * hl);
-          i16x8 v = *(const i16x8*)(qrow + dim);
-          qf[ks] = (head_ok && tok_ok) ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
-        }
-      }
+      // query fragment of the item (first chunk, unless the previous item's last
+      // step loaded it): compiler-visible loads issued before the resolution's
+      // loads, so they land during its memory round trips; the compiler's wait
+      // for the table words below covers them
+      if (c0 == p_lo && !have_q) load_q(tok, head);
       // ---- resolve positions -> cache rows (bit 31: compressed cache) ----
       constexpr int PER = RCH / NT;
       static_assert(PER == 4, "resolution positions per thread");
@@ -757,6 +791,7 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
       //   P·V(b), DMAs of tile a + 3 between its MFMAs (into stage a);
       //   wait for this wave's DMAs of a + 2;  barrier 2 (stage b free, a + 2 in LDS).
       const int npair = (ntile + 1) >> 1;
+      const bool last_chunk = c0 + RCH >= p_hi;
       DmaAddrs nd = next_addrs(2);
       for (int pp = 0; pp < npair; ++pp) {
         const int ta = 2 * pp;
@@ -847,6 +882,12 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
         __syncthreads();             // barrier 2: stage b free; tile a + 2 in LDS
       }
       wait_vmcnt<0>();  // the last (zero-row) DMAs have landed
+      // the item's last Q·Kᵀ has read qf: the next item's query fragment goes out
+      // now and lands under the epilogue (before the output stores, so waiting
+      // for it does not wait for them)
+      if constexpr (PREF) {
+        if (last_chunk) q_pref = prefetch_next_q();
+      }
     }
 
     if (p_lo >= p_hi) m_run = seed_m();  // an item with no rows: the sink alone
@@ -1905,8 +1946,11 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
       if (a.phases & SAS_PHASE_PIPELINED)
         hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
                            dim3(256 * NHG), 0, st, a);
+      else if (a.total_tokens > a.batch)  // some batch holds several query rows
+        hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF, true>), dim3(8 * per_xcd),
+                           dim3(128 * NHG), 0, st, a);
       else
-        hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
+        hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF, false>), dim3(8 * per_xcd),
                            dim3(128 * NHG), 0, st, a);
     }
     hipError_t e = hipGetLastError();
