@@ -342,6 +342,10 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   // latency is not on the start-up chain.
   const float sink_hb0 = hlocal < a.num_heads ? a.sinks[hlocal] : -INFINITY;
   const float sink_hb1 = MB + hlocal < a.num_heads ? a.sinks[MB + hlocal] : -INFINITY;
+  // the lane-held lengths are waited for here, once: read first inside the item
+  // loop, whose later iterations have output stores and query loads in flight,
+  // they would make the head of every item wait for those
+  asm volatile("" ::"v"(lane_aq), "v"(lane_kv), "v"(lane_qp));
   int item_par = 0;  // which first_neg slot the next top-k scan uses
   bool first_item = true;
   // query fragment of this wave's dims half (B operand of Sᵀ = K·Qᵀ); the next
