@@ -113,7 +113,10 @@ int sas_metadata_build_device(int32_t* meta, int batch, const int32_t* act_q,
                               int fd_head_chunk, int reuse, void* stream);
 
 /* Bytes of split-KV partial workspace for a schedule:
- * num_partial_slots * m_base * (head_dim_v + 1) * sizeof(float). */
+ * num_partial_slots * m_base * (2 * head_dim_v + 8): the partials [slot][head][head_dim_v]
+ * as fp16 (acc / l times a power-of-two scale that keeps the row's largest |value|
+ * below 2^15; 1 for rows below that), then [slot][head] fp32 lse and [slot][head]
+ * fp32 inverse scales. */
 int64_t sas_workspace_bytes(int num_partial_slots, int m_base, int head_dim_v);
 
 /* dtype codes */

@@ -95,15 +95,29 @@ def attend_token_kernel_order(q: torch.Tensor, segments: Sequence[torch.Tensor],
     return out, lse
 
 
+def fp16_partial(o: torch.Tensor) -> torch.Tensor:
+    """A split piece's partial rows ``o`` [heads, d_v] (fp32) as the kernels store them:
+    per row, fp16 of ``o * s`` with ``s = 2^(14 - e)`` when the row's largest |value|
+    ``m`` is finite and at least 2^15 (``e = floor(log2 m)``, so ``m * s`` lies in
+    [2^14, 2^15)), else ``s = 1``; returned as fp32 ``fp16(o * s) / s``."""
+    o = o.to(torch.float32)
+    m = o.abs().nan_to_num(nan=0.0).amax(dim=1, keepdim=True)
+    big = (m >= 32768.0) & torch.isfinite(m)
+    e = torch.frexp(torch.where(big, m, torch.ones_like(m)))[1].to(torch.float32) - 1.0
+    s = torch.where(big, torch.exp2(14.0 - e), torch.ones_like(m))
+    return (o * s).to(torch.float16).to(torch.float32) / s
+
+
 def attend_token_split(q: torch.Tensor, segments: Sequence[torch.Tensor], sinks: torch.Tensor,
                        softmax_scale: float, *, d_v: Optional[int] = None, tile: int = 64,
                        pieces: int = 2, partial_dtype: torch.dtype = torch.float32
                        ) -> Tuple[torch.Tensor, torch.Tensor]:
     """One token split into ``pieces`` contiguous pieces of the attended list (cut at
     multiples of ``tile``), each in the kernel's order without the sink, its
-    partial ``acc / l`` rounded to ``partial_dtype``, merged in fp32 as the merge
-    kernel does: lse = m + ln(e^(sink - m) + sum_i e^(lse_i - m)) over
-    m = max(sink, lse_i), out = RNE(sum_i e^(lse_i - lse) o_i)."""
+    partial ``acc / l`` rounded to ``partial_dtype`` (fp16: scaled as the kernels
+    store it, ``fp16_partial``), merged in fp32 as the merge kernel does:
+    lse = m + ln(e^(sink - m) + sum_i e^(lse_i - m)) over m = max(sink, lse_i),
+    out = RNE(sum_i e^(lse_i - lse) o_i)."""
     dtype = q.dtype
     g = q.shape[0]
     dv = q.shape[1] if d_v is None else int(d_v)
@@ -115,8 +129,11 @@ def attend_token_split(q: torch.Tensor, segments: Sequence[torch.Tensor], sinks:
     parts = []
     for lo, hi in zip(cuts, cuts[1:]):
         if hi > lo:
-            parts.append(attend_token_kernel_order(q, [rows[lo:hi]], no_sink, softmax_scale, d_v=dv,
-                                                   tile=tile, tau=0.0, out_dtype=partial_dtype))
+            f16 = partial_dtype == torch.float16
+            o, l = attend_token_kernel_order(q, [rows[lo:hi]], no_sink, softmax_scale, d_v=dv,
+                                             tile=tile, tau=0.0,
+                                             out_dtype=torch.float32 if f16 else partial_dtype)
+            parts.append((fp16_partial(o) if f16 else o, l))
     sink = sinks.to(torch.float32)
     mx = sink.clone()
     for _, l in parts:

@@ -6,7 +6,8 @@ For each random configuration of the GPU sweep (``gen.random_sweep_cfg``, the
 reference's U(-10, 10) inputs) it computes golden (``golden_ref``, 512-row
 tiles), the float64 closed form, golden with 32- and 64-row tiles, and the
 kernel's order (``kernel_order``) for several step sizes, thresholds ``tau``
-and stream counts, split-KV pieces (fp32 / bf16 partials), and reports per variant how many configurations fail the reference's rule
+and stream counts, split-KV pieces (fp32 / bf16 / scaled fp16 partials), and reports per
+variant how many configurations fail the reference's rule
 (>= 99.5 % of elements within rtol 2^-7 / atol 1e-4 of golden) and how many
 have elements beyond atol = rtol = 2e-2 of golden.
 
@@ -37,8 +38,10 @@ VARIANTS = [("golden32", 32, None, 1), ("golden64", 64, None, 1), ("t64_tau0", 6
 
 # split-KV variants: every token's attended list cut into two pieces at a 64-row
 # boundary (each piece golden's own rule at 64-row tiles, without the sink),
-# partials in fp32 or bf16, merged as the merge kernel does
-SPLITS = [("t64_split2_f32", torch.float32), ("t64_split2_bf16", torch.bfloat16)]
+# partials in fp32, bf16 or scaled fp16 (the kernels' format), merged as the merge
+# kernel does
+SPLITS = [("t64_split2_f32", torch.float32), ("t64_split2_bf16", torch.bfloat16),
+          ("t64_split2_f16", torch.float16)]
 
 
 def run_case(i: int) -> dict:

@@ -194,6 +194,26 @@ __device__ void nan_fill(const SasAttnArgs& a, int tid, int nthreads) {
   for (size_t k = tid; k < rows; k += nthreads) a.lse[k] = __builtin_nanf("");
 }
 
+// Split-KV partials: per (slot, head) the row acc / l as fp16, times a power-of-two
+// scale that keeps the row's largest |value| below 2^15 (1 for every row below
+// that), then fp32 lse [slot][head] and fp32 inverse scales [slot][head].
+// fp16's 11-bit significand keeps the merged result as close to golden as fp32
+// partials do on the reference's input distribution, at half the bytes.
+struct PartialScale {
+  float scale, inv;
+};
+__device__ inline PartialScale partial_scale(float row_max) {
+  if (row_max >= 32768.0f && row_max < INFINITY) {
+    const int e = (int)((__float_as_uint(row_max) >> 23) & 0xFF) - 127;  // 15 .. 127
+    return {__uint_as_float((uint32_t)(127 + 14 - e) << 23),
+            __uint_as_float((uint32_t)(127 + e - 14) << 23)};
+  }
+  return {1.0f, 1.0f};
+}
+__device__ inline float* partial_lse(const SasAttnArgs& a, int mb, int dv) {
+  return (float*)((char*)a.workspace + (size_t)a.num_partial_slots * mb * dv * 2);
+}
+
 // fp8 cache rows (SAS_KV_FP8_DS_MLA): eight e4m3 values (one 8-byte word) times
 // their block scale, each product rounded to bf16 (v_cvt_pk_f32_fp8 decodes OCP
 // e4m3 exactly; v_mul_f32 and v_cvt_pk_bf16_f32 round to nearest even).
@@ -934,39 +954,46 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
             a.lse[(size_t)tok * a.num_heads + hb * MB + hl_e] = (m_run + __log2f(l_run)) * LN2;
         }
       } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
-        // fp32 partials (acc / l), staged one dv half (= one wave of each pair) at a time
-        constexpr int HALF = DV / 2;
-        constexpr int SROW = HALF * 4 + 16;
-        constexpr int CPR = HALF * 4 / 16;
-        static_assert(MB * SROW <= NSTG * STAGE_BYTES, "partial staging");
+        // fp16 partials (acc / l, scaled): the row max over both dv halves (lanes
+        // l, l ^ 32 and the partner wave) picks the scale; rows staged whole, as
+        // the outputs are
+        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes)
+        constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
+        static_assert(MB * SROW + 2 * MB * 4 <= NSTG * STAGE_BYTES, "partial staging");
+        float* rmax = (float*)(stg + MB * SROW);
         const bool empty = !(l_run > 0.0f);
         const float inv = empty ? 0.0f : 1.0f / l_run;
-        char* wbase = (char*)(a.workspace + (size_t)slot * MB * DV);
+        float amax = 0.0f;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          if (half) __syncthreads();  // the first half has been read out
-          if (dh == half) {
+        for (int d = 0; d < DVB; ++d)
 #pragma unroll
-            for (int d = 0; d < DVB; ++d)
+          for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(acc[d][j]));
+        // max |acc| times inv is max |acc * inv| (rounding is monotonic)
+        amax = wave_max_pair(amax) * inv;
+        if (hl == 0) rmax[dh * MB + hl_e] = amax;
+        __syncthreads();
+        const PartialScale ps = partial_scale(fmaxf(rmax[hl_e], rmax[MB + hl_e]));
 #pragma unroll
-              for (int g4 = 0; g4 < 4; ++g4) {
-                const int dv = dv_e - half * HALF + 32 * d + 8 * g4;  // within the half
-                f32x4 v;
+        for (int d = 0; d < DVB; ++d)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[d][4 * g4 + e] * inv;
-                *(f32x4*)(stg + hl_e * SROW + dv * 4) = v;
-              }
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int dv = dv_e + 32 * d + 8 * g4;
+            i16x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              v[e] = __builtin_bit_cast(short, (_Float16)(acc[d][4 * g4 + e] * inv * ps.scale));
+            *(i16x4*)(stg + hl_e * SROW + dv * 2) = v;
           }
-          __syncthreads();
-          for (int c = tid_e; c < nh * CPR; c += NT) {
-            const int h = c / CPR, c16 = c - h * CPR;
-            *(f32x4*)(wbase + ((size_t)h * DV + half * HALF) * 4 + c16 * 16) =
-                *(const f32x4*)(stg + h * SROW + c16 * 16);
-          }
+        __syncthreads();
+        char* wbase = (char*)a.workspace + (size_t)slot * MB * DV * 2;
+        for (int c = tid_e; c < nh * CPR; c += NT) {
+          const int h = c / CPR, c16 = c - h * CPR;
+          *(i16x8*)(wbase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
         }
         if (dh == 0 && hl == 0 && head_ok) {
-          float* wl = a.workspace + (size_t)a.num_partial_slots * MB * DV;
+          float* wl = partial_lse(a, MB, DV);
           wl[(size_t)slot * MB + hl_e] = empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
+          wl[(size_t)(a.num_partial_slots + slot) * MB + hl_e] = ps.inv;
         }
       }
     }
@@ -1730,39 +1757,46 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
             a.lse[(size_t)tok * a.num_heads + hb * MB + hl_e] = (m_fin + __log2f(l_run)) * LN2;
         }
       } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
-        // fp32 partials (acc / l), staged one dv half (waves wq = 2 half, 2 half + 1) at a time
-        constexpr int HALF = DV / 2;
-        constexpr int SROW = HALF * 4 + 16;
-        constexpr int CPR = HALF * 4 / 16;
-        static_assert(MB * SROW <= NSTG * STAGE_BYTES, "partial staging");
+        // fp16 partials (acc / l, scaled): the row max over the four dv quarters
+        // (lanes l, l ^ 32 of waves wq = 0..3) picks the scale; rows staged whole
+        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes), as for the outputs
+        constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
+        static_assert(MB * SROW + 4 * MB * 4 <= NSTG * STAGE_BYTES, "partial staging");
+        float* rmax = (float*)(stg + MB * SROW);
         const bool empty = !(l_run > 0.0f);
         const float inv = empty ? 0.0f : 1.0f / l_run;
-        char* wbase = (char*)(a.workspace + (size_t)slot * MB * DV);
+        float amax = 0.0f;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          if (half) __syncthreads();  // the first half has been read out
-          if ((wq >> 1) == half) {
+        for (int d = 0; d < DVB; ++d)
 #pragma unroll
-            for (int d = 0; d < DVB; ++d)
+          for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(acc[d][j]));
+        // max |acc| times inv is max |acc * inv| (rounding is monotonic)
+        amax = wave_max_pair(amax) * inv;
+        if (hl == 0) rmax[wq * MB + hl_e] = amax;
+        __syncthreads();
+        const PartialScale ps = partial_scale(fmaxf(fmaxf(rmax[hl_e], rmax[MB + hl_e]),
+                                                    fmaxf(rmax[2 * MB + hl_e], rmax[3 * MB + hl_e])));
 #pragma unroll
-              for (int q4 = 0; q4 < 4; ++q4) {
-                const int dv = dv_e - half * HALF + 32 * d + 8 * q4;  // within the half
-                f32x4 v;
+        for (int d = 0; d < DVB; ++d)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[d][4 * q4 + e] * inv;
-                *(f32x4*)(stg + hl_e * SROW + dv * 4) = v;
-              }
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int dv = dv_e + 32 * d + 8 * q4;
+            i16x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              v[e] = __builtin_bit_cast(short, (_Float16)(acc[d][4 * q4 + e] * inv * ps.scale));
+            *(i16x4*)(stg + hl_e * SROW + dv * 2) = v;
           }
-          __syncthreads();
-          for (int c = tid_e; c < nh * CPR; c += NT) {
-            const int h = c / CPR, c16 = c - h * CPR;
-            *(f32x4*)(wbase + ((size_t)h * DV + half * HALF) * 4 + c16 * 16) =
-                *(const f32x4*)(stg + h * SROW + c16 * 16);
-          }
+        __syncthreads();
+        char* wbase = (char*)a.workspace + (size_t)slot * MB * DV * 2;
+        for (int c = tid_e; c < nh * CPR; c += NT) {
+          const int h = c / CPR, c16 = c - h * CPR;
+          *(i16x8*)(wbase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
         }
         if (wq == 0 && hl == 0 && head_p_ok) {
-          float* wl = a.workspace + (size_t)a.num_partial_slots * MB * DV;
+          float* wl = partial_lse(a, MB, DV);
           wl[(size_t)slot * MB + hl_e] = empty ? -INFINITY : (m_fin + __log2f(l_run)) * LN2;
+          wl[(size_t)(a.num_partial_slots + slot) * MB + hl_e] = ps.inv;
         }
       }
     }
@@ -1808,15 +1842,20 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
   // rows past the task's last head (never stored) read that head's row instead
   const int hr = g0 + hh < hn ? g0 + hh : hn - 1;
   const int hloc = h0 + hr;                            // m-block slot of this thread's row
-  const float* wo = a.workspace;
-  const float* wl = a.workspace + (size_t)a.num_partial_slots * mb * DV;
+  const _Float16* wo = (const _Float16*)a.workspace;
+  const float* wl = partial_lse(a, mb, DV);
+  const float* wsc = wl + (size_t)a.num_partial_slots * mb;  // inverse scales
+  typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
   auto piece = [&](int i, f32x4 (&v)[PER]) {
-    const float* src = wo + ((size_t)(slot0 + i) * mb + hloc) * DV + 4 * c0;
+    const _Float16* src = wo + ((size_t)(slot0 + i) * mb + hloc) * DV + 4 * c0;
 #pragma unroll
-    for (int k = 0; k < PER; ++k)  // all of one piece's loads in flight together
-      v[k] = *(const f32x4*)(src + 4 * TPH * k);
+    for (int k = 0; k < PER; ++k) {  // all of one piece's loads in flight together
+      const h16x4 x = *(const h16x4*)(src + 4 * TPH * k);
+      v[k] = (f32x4){(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+    }
   };
   auto plse = [&](int i) -> float { return wl[(size_t)(slot0 + i) * mb + hloc]; };
+  auto pinv = [&](int i) -> float { return wsc[(size_t)(slot0 + i) * mb + hloc]; };
   const int s = m / hblocks;
   const int h = (m - s * hblocks) * mb + hloc;  // query head
   const bool store = g0 + hh < hn && h < a.num_heads;
@@ -1836,6 +1875,8 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
     if (npc > 1) piece(1, v1);
     const float l0 = plse(0);
     const float l1 = npc > 1 ? plse(1) : -INFINITY;
+    const float s0 = pinv(0);
+    const float s1 = npc > 1 ? pinv(1) : 1.0f;
     float mx = fmaxf(sink, l0);
     if (npc > 1) mx = fmaxf(mx, l1);
     if (mx != -INFINITY) {  // else no key and no sink: lse -inf, every weight 0
@@ -1843,12 +1884,12 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
       if (npc > 1) tot += __expf(l1 - mx);
       l = mx + __logf(tot);
     }
-    const float w0 = weight(l0);
+    const float w0 = weight(l0) * s0;  // the piece's inverse scale is a power of two
 #pragma unroll
     for (int k = 0; k < PER; ++k)
       o[k] = (f32x4){w0 * v0[k][0], w0 * v0[k][1], w0 * v0[k][2], w0 * v0[k][3]};
     if (npc > 1) {
-      const float w1 = weight(l1);
+      const float w1 = weight(l1) * s1;
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
         o[k][0] += w1 * v1[k][0]; o[k][1] += w1 * v1[k][1];
@@ -1862,8 +1903,12 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
     constexpr int PB = 4;
     constexpr int MAXL = 16;
     f32x4 vb[PB][PER];
+    float sb[PB];
 #pragma unroll
-    for (int i = 0; i < PB; ++i) piece(i < npc ? i : npc - 1, vb[i]);
+    for (int i = 0; i < PB; ++i) {
+      piece(i < npc ? i : npc - 1, vb[i]);
+      sb[i] = pinv(i < npc ? i : npc - 1);
+    }
     float lv[MAXL];
 #pragma unroll
     for (int i = 0; i < MAXL; ++i) lv[i] = plse(i < npc ? i : npc - 1);
@@ -1884,12 +1929,15 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
     for (int i0 = 0; i0 < npc; i0 += PB) {
       if (i0 > 0) {
 #pragma unroll
-        for (int i = 0; i < PB; ++i) piece(i0 + i < npc ? i0 + i : npc - 1, vb[i]);
+        for (int i = 0; i < PB; ++i) {
+          piece(i0 + i < npc ? i0 + i : npc - 1, vb[i]);
+          sb[i] = pinv(i0 + i < npc ? i0 + i : npc - 1);
+        }
       }
 #pragma unroll
       for (int i = 0; i < PB; ++i) {
         if (i0 + i >= npc) break;
-        const float wi = weight(lse_of(i0 + i));
+        const float wi = weight(lse_of(i0 + i)) * sb[i];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
           if (i0 + i == 0) {

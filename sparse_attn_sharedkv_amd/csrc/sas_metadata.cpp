@@ -263,5 +263,6 @@ extern "C" int sas_metadata_build(int32_t* meta, int batch, const int32_t* act_q
 
 extern "C" int64_t sas_workspace_bytes(int num_partial_slots, int m_base, int head_dim_v) {
   if (num_partial_slots < 0 || m_base < 0 || head_dim_v < 0) return 0;
-  return (int64_t)num_partial_slots * m_base * (head_dim_v + 1) * (int64_t)sizeof(float);
+  // fp16 partials, then fp32 lse and fp32 inverse scales
+  return (int64_t)num_partial_slots * m_base * (2 * (int64_t)head_dim_v + 8);
 }

@@ -299,3 +299,23 @@ def test_split_item_without_sink_and_without_keys():
     assert torch.equal(out[1].float().cpu(), torch.zeros_like(out[1].float().cpu()))
     assert torch.isneginf(lse[1]).all()
     _check_benchmark_regime(out, lse, kw)
+
+
+@requires_gpu
+def test_split_partials_of_large_values():
+    # split-KV partials are stored as fp16 scaled by a power of two per (piece, head)
+    # row; cache values of 2^24 times the usual size (q scaled down by as much, so
+    # the scores are the usual ones) make the partial rows exceed fp16's range
+    # unless scaled. Golden is exactly 2^24 times golden on the unscaled inputs
+    # (power-of-two scalings commute with every rounding), so the result divided by
+    # 2^24 is checked against golden on those, with every item split.
+    _say("split partials of large values")
+    kw = _reduced_workload("mla_decode_b64_h128_k2048", 2, seed=13)
+    big = dict(kw)
+    for key in ("ori_kv", "cmp_kv"):
+        big[key] = kw[key] * 2.0 ** 24
+    big["q"] = kw["q"] * 2.0 ** -24
+    out, lse = _run(big, fn=sparse_flash_mla, core_num=256)
+    assert torch.isfinite(out.float()).all()
+    assert out.float().abs().max() > 2.0 ** 16  # beyond fp16's range
+    _check_benchmark_regime((out.float() * 2.0 ** -24).to(out.dtype), lse, kw)

@@ -85,7 +85,8 @@ def test_device_scheduler_rejects_bad_arguments_without_a_gpu():
 
 def test_workspace_bytes():
     lib = _lib.load()
-    assert lib.sas_workspace_bytes(256, 64, 512) == 256 * 64 * 513 * 4
+    # fp16 partials, fp32 lse and fp32 inverse scales per (slot, head)
+    assert lib.sas_workspace_bytes(256, 64, 512) == 256 * 64 * (512 * 2 + 4 + 4)
     assert lib.sas_workspace_bytes(-1, 64, 512) == 0
 
 

@@ -130,3 +130,53 @@ def test_split_pieces_merge_like_the_closed_form():
     d = (o2.float() - torch.from_numpy(om).float()).abs()
     assert (d <= torch.finfo(torch.bfloat16).eps * torch.from_numpy(np.abs(om)).float() + 1e-6).all()
     assert np.allclose(l2.numpy(), lm, rtol=1e-5, atol=1e-5)
+
+
+def test_fp16_partials_keep_their_scale():
+    # the kernels' split-KV partial format (fp16_partial): rows below 2^15 are plain
+    # fp16 of the value; larger rows (bf16 caches can hold values up to ~3e38) are
+    # scaled by a power of two into [2^14, 2^15) and stay finite, with fp16's
+    # relative precision against the row's largest value
+    from oracle.kernel_order import fp16_partial
+    g = torch.Generator().manual_seed(3)
+    small = torch.randn(8, 512, generator=g) * 100.0
+    assert torch.equal(fp16_partial(small), small.to(torch.float16).to(torch.float32))
+    for mag in (2.0 ** 15, 2.0 ** 15 * 1.999, 1e6, 3e38):
+        o = torch.randn(4, 512, generator=g)
+        o = o / o.abs().amax(dim=1, keepdim=True) * mag
+        o = o.clamp(-3.3e38, 3.3e38)
+        r = fp16_partial(o)
+        assert torch.isfinite(r).all()
+        m = o.abs().amax(dim=1, keepdim=True)
+        # scaled into [2^14, 2^15), where fp16's half spacing is 8: every element
+        # within 2^-11 of the row max, the row max itself within 2^-12 relative
+        assert ((r - o).abs() <= m * 2.0 ** -11).all(), mag
+        assert ((r.abs().amax(dim=1, keepdim=True) - m).abs() <= m * 2.0 ** -12).all(), mag
+    # NaN elements stay NaN and do not pick the scale; infinities stay infinite
+    o = torch.ones(2, 8) * 40000.0
+    o[0, 3] = float("nan")
+    o[1, 2] = float("inf")
+    r = fp16_partial(o)
+    assert torch.isnan(r[0, 3]) and torch.isinf(r[1, 2])
+    assert torch.allclose(r[0, :3], o[0, :3], rtol=2 ** -11)
+
+
+def test_split_with_fp16_partials_matches_fp32_partials():
+    # on the reference's input distribution the fp16 partials change the merged
+    # result by at most fp16's rounding of the pieces (2^-11 of the row's largest
+    # value, twice for the weights summing to 1 in the worst case) plus one bf16
+    # rounding step of the fp32-partial result, and only in a few elements
+    from oracle.kernel_order import attend_token_split
+    g = torch.Generator().manual_seed(11)
+    q = ((torch.rand(64, 512, generator=g) * 20 - 10)).to(torch.bfloat16)
+    rows = ((torch.rand(900, 512, generator=g) * 20 - 10)).to(torch.bfloat16)
+    sinks = torch.rand(64, generator=g) * 2 - 1
+    scale = 1 / math.sqrt(512)
+    o32, l32 = attend_token_split(q, [rows], sinks, scale, d_v=512, pieces=3)
+    o16, l16 = attend_token_split(q, [rows], sinks, scale, d_v=512, pieces=3,
+                                  partial_dtype=torch.float16)
+    assert torch.equal(l16, l32)
+    d = (o16.float() - o32.float()).abs()
+    row = o32.float().abs().amax(dim=1, keepdim=True)
+    assert (d <= 2.0 ** -10 * row + torch.finfo(torch.bfloat16).eps * o32.float().abs()).all()
+    assert (d > 0).float().mean() < 0.05

@@ -65,7 +65,8 @@ def test_noalloc_refuses_a_workspace_beyond_the_scratch():
     kw = gen.build_workload("mla_decode_b64_h128_k2048", device="cuda", seed=3, batch=2)
     prep = api.prepare(**kw, core_num=256)
     a = _lib.SasAttnArgs.from_buffer_copy(prep.args)
-    a.num_partial_slots = _lib.NOALLOC_SCRATCH_BYTES // (a.m_base * (a.head_dim_v + 1) * 4) + 1
+    per_slot = _lib.load().sas_workspace_bytes(1, a.m_base, a.head_dim_v)
+    a.num_partial_slots = _lib.NOALLOC_SCRATCH_BYTES // per_slot + 1
     rc = _lib.load().sas_attention_launch_noalloc(ctypes.byref(a), None)
     assert rc == _lib.SAS_E_CAPACITY
     assert "scratch" in _lib.last_error()
