@@ -928,7 +928,7 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
       int tid_e = tid, hl_e = hlocal, dv_e = dh * (DV / 2) + 4 * hl;
       asm volatile("" : "+v"(tid_e), "+v"(hl_e), "+v"(dv_e));
       if (!partial) {
-        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes)
+        constexpr int SROW = DV * 2 + 16;  // staging row stride (bytes; 16-byte aligned rows)
         constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
         static_assert(MB * SROW <= NSTG * STAGE_BYTES, "output staging");
         const float inv = 1.0f / l_run;
@@ -957,7 +957,7 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
         // fp16 partials (acc / l, scaled): the row max over both dv halves (lanes
         // l, l ^ 32 and the partner wave) picks the scale; rows staged whole, as
         // the outputs are
-        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes)
+        constexpr int SROW = DV * 2 + 16;  // staging row stride (bytes; 16-byte aligned rows)
         constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
         static_assert(MB * SROW + 2 * MB * 4 <= NSTG * STAGE_BYTES, "partial staging");
         float* rmax = (float*)(stg + MB * SROW);
@@ -1731,7 +1731,7 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       int tid_e = tid, hl_e = hp, dv_e = wq * DVQ + 4 * hl;
       asm volatile("" : "+v"(tid_e), "+v"(hl_e), "+v"(dv_e));
       if (!partial) {
-        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes)
+        constexpr int SROW = DV * 2 + 16;  // staging row stride (bytes; 16-byte aligned rows)
         constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
         static_assert(MB * SROW <= NSTG * STAGE_BYTES, "output staging");
         const float inv = 1.0f / l_run;
@@ -1759,7 +1759,7 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
         // fp16 partials (acc / l, scaled): the row max over the four dv quarters
         // (lanes l, l ^ 32 of waves wq = 0..3) picks the scale; rows staged whole
-        constexpr int SROW = DV * 2 + 8;   // staging row stride (bytes), as for the outputs
+        constexpr int SROW = DV * 2 + 16;  // staging row stride (bytes), as for the outputs
         constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
         static_assert(MB * SROW + 4 * MB * 4 <= NSTG * STAGE_BYTES, "partial staging");
         float* rmax = (float*)(stg + MB * SROW);
@@ -1812,8 +1812,9 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
 // Split-KV merge: lse = log(e^sink + Σ e^lse_i), out = Σ e^(lse_i - lse) o_i
 // ---------------------------------------------------------------------------
 // Grid: (merge task, group of MERGE_HPB heads). Thread t owns head t / 32 of
-// the group and float4 columns (t % 32) + 32 k: a half-wave reads 512
-// contiguous bytes per load. Each thread derives its head's weights itself
+// the group and the 8-column chunks (t % 32) + 32 k of its row (one 16-byte
+// load of fp16 partials, one 16-byte store of outputs each): a half-wave reads
+// 512 contiguous bytes per load. Each thread derives its head's weights itself
 // (the piece lse values are the same words for its 32 lanes), so there is no
 // LDS and no barrier, and the first two pieces' loads are in flight with the
 // lse, sink and token loads.
@@ -1825,7 +1826,7 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
   constexpr int V4 = DV / 4;                              // float4 per head row
   constexpr int TPH = MERGE_THREADS / MERGE_HPB;          // threads per head (32)
   constexpr int PER = V4 / TPH;                           // float4 per thread (4)
-  static_assert(V4 % TPH == 0 && TPH <= 64 && 64 % TPH == 0, "merge tiling");
+  static_assert(V4 % (2 * TPH) == 0 && TPH <= 64 && 64 % TPH == 0, "merge tiling");
   const int32_t* fd = a.metadata + SAS_FD_OFFSET + task * SAS_FD_METADATA_SIZE;
   if (fd[0] == 0) return;
   const int mb = a.m_base;
@@ -1846,12 +1847,14 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
   const float* wl = partial_lse(a, mb, DV);
   const float* wsc = wl + (size_t)a.num_partial_slots * mb;  // inverse scales
   typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
   auto piece = [&](int i, f32x4 (&v)[PER]) {
-    const _Float16* src = wo + ((size_t)(slot0 + i) * mb + hloc) * DV + 4 * c0;
+    const _Float16* src = wo + ((size_t)(slot0 + i) * mb + hloc) * DV + 8 * c0;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {  // all of one piece's loads in flight together
-      const h16x4 x = *(const h16x4*)(src + 4 * TPH * k);
-      v[k] = (f32x4){(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+    for (int k = 0; k < PER / 2; ++k) {  // all of one piece's loads in flight together
+      const h16x8 x = *(const h16x8*)(src + 8 * TPH * k);
+      v[2 * k] = (f32x4){(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+      v[2 * k + 1] = (f32x4){(float)x[4], (float)x[5], (float)x[6], (float)x[7]};
     }
   };
   auto plse = [&](int i) -> float { return wl[(size_t)(slot0 + i) * mb + hloc]; };
@@ -1951,12 +1954,14 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
     }
   }
   if (!store || tok < 0 || tok >= a.total_tokens) return;
-  T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 4 * c0;
+  T* orow = (T*)a.out + ((size_t)tok * a.num_heads + h) * DV + 8 * c0;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const i16x4 pk = {MfmaOps<T>::from_f32(o[k][0]), MfmaOps<T>::from_f32(o[k][1]),
-                      MfmaOps<T>::from_f32(o[k][2]), MfmaOps<T>::from_f32(o[k][3])};
-    *(i16x4*)(orow + 4 * TPH * k) = pk;
+  for (int k = 0; k < PER / 2; ++k) {
+    const i16x8 pk = {MfmaOps<T>::from_f32(o[2 * k][0]), MfmaOps<T>::from_f32(o[2 * k][1]),
+                      MfmaOps<T>::from_f32(o[2 * k][2]), MfmaOps<T>::from_f32(o[2 * k][3]),
+                      MfmaOps<T>::from_f32(o[2 * k + 1][0]), MfmaOps<T>::from_f32(o[2 * k + 1][1]),
+                      MfmaOps<T>::from_f32(o[2 * k + 1][2]), MfmaOps<T>::from_f32(o[2 * k + 1][3])};
+    *(i16x8*)(orow + 8 * TPH * k) = pk;
   }
   if (c0 == 0) a.lse[(size_t)tok * a.num_heads + h] = l;
 }
