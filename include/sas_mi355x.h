@@ -173,7 +173,16 @@ typedef struct SasAttnArgs {
    * SAS_PHASE_PIPELINED (bit 2) runs native rows through the attention kernel
    * that fp8 rows use (two waves per SIMD, software-pipelined); by default native
    * rows take the one-wave-per-SIMD kernel, which is faster on them. Results of the
-   * two kernels agree to within rounding, not bit for bit. */
+   * two kernels agree to within rounding, not bit for bit.
+   * SAS_PHASE_FP8_QK (bit 3, fp8 rows only) forms Q·Kᵀ on fp8 MFMA
+   * (v_mfma_f32_16x16x128_f8f6f4): each head's 512 latent query dims are quantized
+   * to e4m3 with one fp32 scale (amax / 448, q / scale rounded to nearest even), the
+   * cache rows' e4m3 dims are used as stored, and each row's 128-dim block scales and
+   * the head's scale are applied to the four block dot products in fp32; the rope
+   * dims stay bf16. P·V stays on the dequantized bf16 rows. No reference counterpart
+   * (kernel.py:2036-2352 forms Q·Kᵀ in bf16): it adds the query's quantization error,
+   * which is small against golden for N(0,1)-scaled data but not for the reference
+   * tests' U(-10, 10) data, so it is opt-in. */
   int32_t phases;
   /* row format of ori_kv and cmp_kv: SAS_KV_NATIVE or SAS_KV_FP8_DS_MLA */
   int32_t kv_format;
@@ -193,6 +202,7 @@ int sas_attention_launch(const SasAttnArgs* args, void* stream);
  * one device share its scratch array: calls that may overlap on one device (other
  * streams, concurrent threads) race and must be serialised by the caller. */
 #define SAS_PHASE_PIPELINED 4
+#define SAS_PHASE_FP8_QK 8
 #define SAS_NOALLOC_SCRATCH_BYTES (72ull << 20)
 int sas_attention_launch_noalloc(const SasAttnArgs* args, void* stream);
 

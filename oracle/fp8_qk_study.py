@@ -28,7 +28,7 @@ import sys
 import numpy as np
 import torch
 
-from .fp8_rows import E4M3_MAX, LATENT, BLOCK, ROPE, decode_e4m3, encode_e4m3, quantize_rows
+from .fp8_rows import LATENT, BLOCK, ROPE, decode_e4m3, quantize_rows, scores_fp8
 
 LOG2E = 1.4426950408889634
 
@@ -58,32 +58,6 @@ def golden_softmax_pv(s: np.ndarray, v: np.ndarray, tile: int = 512):
 def scores_bf16(q: np.ndarray, k: np.ndarray, scale: float) -> np.ndarray:
     """Golden's scores: bf16 query and dequantized bf16 rows, fp32 products."""
     return (q.astype(np.float32) @ k.T.astype(np.float32)) * np.float32(scale)
-
-
-def quantize_q(q: np.ndarray):
-    """Per head: e4m3 codes of q[:, :512] / s_q with s_q = amax / 448 (1 for zero heads)."""
-    lat = q[:, :LATENT].astype(np.float32)
-    amax = np.abs(lat).max(axis=1)
-    sq = np.where(amax > 0, amax / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
-    codes = encode_e4m3(np.clip(lat / sq[:, None], -E4M3_MAX, E4M3_MAX).astype(np.float32))
-    return codes, sq
-
-
-def scores_fp8(q: np.ndarray, raw: np.ndarray, scale: float) -> np.ndarray:
-    """fp8 Q·Kᵀ: per-block e4m3 dot products times both scales, plus the bf16 rope part."""
-    codes, sq = quantize_q(q)
-    q8 = decode_e4m3(codes).astype(np.float64)                        # exact values
-    k8 = decode_e4m3(raw[:, :LATENT]).astype(np.float64)
-    sk = np.ascontiguousarray(raw[:, 512:528]).view("<f4").reshape(-1, 4).astype(np.float64)
-    s = np.zeros((q.shape[0], raw.shape[0]), dtype=np.float64)
-    for blk in range(LATENT // BLOCK):
-        sl = slice(blk * BLOCK, (blk + 1) * BLOCK)
-        s += (q8[:, sl] @ k8[:, sl].T) * sk[None, :, blk]
-    s *= sq[:, None].astype(np.float64)
-    rope_k = torch.from_numpy(np.ascontiguousarray(raw[:, 528:]).view("<i2").astype(np.int16)) \
-        .view(torch.bfloat16).float().numpy()
-    s += q[:, LATENT:].astype(np.float64) @ rope_k.T.astype(np.float64)
-    return (s * scale).astype(np.float32)
 
 
 def dequant_bf16(raw: np.ndarray) -> np.ndarray:

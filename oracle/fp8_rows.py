@@ -27,6 +27,15 @@ pinned by the format's definition and by library routines instead (tests in
                       exactly like the bf16 cache this function returns, so the
                       attention oracle for fp8 caches is ``golden_ref`` on the
                       dequantized pool.
+* ``quantize_q``      the fp8 Q·Kᵀ form's query: per head, codes of
+                      q * (448 / amax) (fp32 division, fp32 product, clamp,
+                      RNE) and sq = amax / 448; checked against torch's cast.
+* ``scores_fp8``      that form's scores (float64): sq * sum over the four
+                      128-dim blocks of the row scale times the e4m3 dot
+                      product, plus the bf16 rope dot product; checked against
+                      the float64 product of the dequantized operands and,
+                      with power-of-two scales and e4m3-exact queries, against
+                      golden's scores on the dequantized bf16 rows exactly.
 """
 
 from __future__ import annotations
@@ -147,3 +156,50 @@ def random_rows(n: int, gen: torch.Generator, scale_range=(1e-3, 1e-2)) -> np.nd
     rope = (torch.randn((n, ROPE), generator=gen) * 0.5).to(torch.bfloat16)
     out[:, ROPE_OFF:] = rope.view(torch.int16).numpy().astype("<i2").view(np.uint8).reshape(n, 128)
     return out
+
+
+def quantize_q(q) -> tuple:
+    """``[G, >=512]`` query heads (bf16 values) -> (e4m3 codes ``[G, 512]``, sq ``[G]`` fp32).
+
+    The fp8 Q·Kᵀ form's per-head quantization of the 512 latent dims:
+    ``inv = 448 / amax`` (IEEE fp32 division; 1 for an all-zero head), codes =
+    ``rne_e4m3(clamp(x * inv, -448, 448))`` with the product in fp32, and the
+    scale the scores are multiplied back by, ``sq = amax / 448`` (1 for a zero head).
+    """
+    if isinstance(q, torch.Tensor):
+        q = q.to(torch.float32).cpu().numpy()
+    lat = np.asarray(q, dtype=np.float32)[:, :LATENT]
+    amax = np.abs(lat).max(axis=1)
+    nz = amax > 0
+    safe = np.where(nz, amax, np.float32(1.0)).astype(np.float32)
+    inv = np.where(nz, np.float32(E4M3_MAX) / safe, np.float32(1.0)).astype(np.float32)
+    sq = np.where(nz, safe / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
+    v = np.clip((lat * inv[:, None]).astype(np.float32), np.float32(-E4M3_MAX), np.float32(E4M3_MAX))
+    return encode_e4m3(v), sq
+
+
+def scores_fp8(q, raw, scale: float) -> np.ndarray:
+    """Scores ``[G, n]`` (float32, times ``scale``) of the fp8 Q·Kᵀ form over raw rows ``[n, 656]``.
+
+    ``s = sq * sum_blk sk[blk] * (q8[blk] . k8[blk]) + q_rope . k_rope`` in float64
+    (e4m3 values and their products are exact there), the rope dims as bf16.
+    """
+    if isinstance(q, torch.Tensor):
+        q = q.to(torch.float32).cpu().numpy()
+    q = np.asarray(q, dtype=np.float32)
+    if isinstance(raw, torch.Tensor):
+        raw = raw.cpu().view(torch.uint8).numpy()
+    raw = np.ascontiguousarray(np.asarray(raw, dtype=np.uint8)).reshape(-1, ROW_BYTES)
+    codes, sq = quantize_q(q)
+    q8 = decode_e4m3(codes).astype(np.float64)
+    k8 = decode_e4m3(raw[:, :LATENT]).astype(np.float64)
+    sk = np.ascontiguousarray(raw[:, SCALE_OFF:ROPE_OFF]).view("<f4").reshape(-1, 4).astype(np.float64)
+    s = np.zeros((q.shape[0], raw.shape[0]), dtype=np.float64)
+    for blk in range(LATENT // BLOCK):
+        sl = slice(blk * BLOCK, (blk + 1) * BLOCK)
+        s += (q8[:, sl] @ k8[:, sl].T) * sk[None, :, blk]
+    s *= sq[:, None].astype(np.float64)
+    rope_k = torch.from_numpy(np.ascontiguousarray(raw[:, ROPE_OFF:]).view("<i2").astype(np.int16)) \
+        .view(torch.bfloat16).double().numpy()
+    s += q[:, LATENT:].astype(np.float64) @ rope_k.T
+    return (s * scale).astype(np.float32)

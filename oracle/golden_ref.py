@@ -23,6 +23,12 @@ Follows ``golden.py`` (reference) function by function:
 * fp8 caches (656-byte rows, no reference counterpart): rows are gathered
   raw and dequantized with ``fp8_rows.dequantize_rows``; everything after
   is the bf16 math above
+* ``attend_token_scores``    ``attend_token`` on precomputed scores (the same
+                              tiles, sink, rounding and state); with golden's
+                              scores it equals ``attend_token`` bit for bit
+* ``attend_token_fp8qk``     the fp8 Q·Kᵀ form (``fp8_qk=True``, no reference
+                              counterpart): scores from ``fp8_rows.scores_fp8``
+                              on the raw rows, P·V on the dequantized rows
 * ``merge_partials``         the closed-form split-KV merge
                               lse = log(e^sink + Σ e^lse_i),
                               o = Σ e^(lse_i - lse) · o_i
@@ -167,6 +173,57 @@ def attend_token(q: torch.Tensor, segments: Sequence[torch.Tensor], sinks: torch
     return out, lse
 
 
+def attend_token_scores(scores: Sequence[torch.Tensor], values: Sequence[torch.Tensor],
+                        sinks: torch.Tensor, dtype: torch.dtype,
+                        tile: int = GOLDEN_S2_TILE) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``attend_token``'s online softmax on given scores (golden.py:156-200).
+
+    ``scores[i]``: ``[G, n_i]`` fp32 scores of segment i, already multiplied by
+    the softmax scale; ``values[i]``: ``[n_i, d_v]`` value rows (input dtype
+    values). Same 512-row tiles per segment, sink seeding, P rounded to
+    ``dtype`` before P·V and fp32 state as ``attend_token``.
+    """
+    g = scores[0].shape[0] if scores else sinks.shape[0]
+    dv = values[0].shape[1]
+    row_max = sinks.to(torch.float32).clone()
+    row_sum = torch.ones(g, dtype=torch.float32)
+    acc = torch.zeros((g, dv), dtype=torch.float32)
+    for sc_seg, v_seg in zip(scores, values):
+        if sc_seg.shape[1] == 0:
+            continue
+        vf = v_seg.to(torch.float32)
+        for t0 in range(0, sc_seg.shape[1], tile):
+            score = sc_seg[:, t0:t0 + tile].to(torch.float32)
+            new_max = torch.maximum(row_max, score.amax(dim=1))
+            alpha = torch.exp(row_max - new_max)
+            p = torch.exp(score - new_max[:, None])
+            row_sum = alpha * row_sum + p.sum(dim=1)
+            p_in = p.to(dtype).to(torch.float32)
+            acc = acc * alpha[:, None] + p_in @ vf[t0:t0 + tile]
+            row_max = new_max
+    out = (acc / row_sum[:, None]).to(dtype)
+    lse = row_max + torch.log(row_sum)
+    return out, lse
+
+
+def attend_token_fp8qk(q: torch.Tensor, raw_segments: Sequence[torch.Tensor], sinks: torch.Tensor,
+                       softmax_scale: float, *, d_v: int = 512,
+                       tile: int = GOLDEN_S2_TILE) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One token under the fp8 Q·Kᵀ form: scores from ``fp8_rows.scores_fp8`` on the
+    raw 656-byte rows (per-head e4m3 query, per-block row scales), then golden's
+    softmax and P·V on the dequantized bf16 rows (``attend_token_scores``)."""
+    from .fp8_rows import dequantize_rows, scores_fp8
+    scores, values = [], []
+    for raw in raw_segments:
+        if raw.shape[0] == 0:
+            scores.append(torch.zeros((q.shape[0], 0), dtype=torch.float32))
+            values.append(torch.zeros((0, d_v), dtype=q.dtype))
+            continue
+        scores.append(torch.from_numpy(scores_fp8(q.to(torch.float32).numpy(), raw, softmax_scale)))
+        values.append(dequantize_rows(raw)[:, :d_v])
+    return attend_token_scores(scores, values, sinks, q.dtype, tile=tile)
+
+
 def one_shot_reference(q: np.ndarray, rows: np.ndarray, sinks: np.ndarray,
                        softmax_scale: float) -> Tuple[np.ndarray, np.ndarray]:
     """float64 closed form ``softmax(scores ∪ sink) · V`` (golden.py:207-244 semantics).
@@ -238,10 +295,12 @@ def _is_fp8_pool(pool, kv_cache_dtype) -> bool:
 
 def token_rows(*, b: int, s: int, act_q: int, act_kv: int, ori_kv, ori_block_table,
                cmp_kv, cmp_block_table, cmp_idx_row, cmp_ratio, ori_win_left,
-               ori_win_right=0, kv_cache_dtype=None) -> Tuple[torch.Tensor, torch.Tensor]:
+               ori_win_right=0, kv_cache_dtype=None,
+               raw: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """The two row segments (window rows, compressed rows) one query attends.
 
-    fp8 pools (656-byte rows) are gathered raw and returned dequantized to bf16.
+    fp8 pools (656-byte rows) are gathered raw and returned dequantized to bf16
+    (or raw, with ``raw=True``).
     """
     s_glob = causal_position(act_kv, act_q, s)
     lo, hi = window_range(s_glob, ori_win_left, ori_win_right)
@@ -254,7 +313,7 @@ def token_rows(*, b: int, s: int, act_q: int, act_kv: int, ori_kv, ori_block_tab
     else:
         cmp_rows = gather_paged_rows(cmp_kv, cmp_block_table, b,
                                      resolve_topk_rows(cmp_idx_row, act_kv, act_q, s, cmp_ratio))
-    if _is_fp8_pool(ori_kv, kv_cache_dtype):
+    if _is_fp8_pool(ori_kv, kv_cache_dtype) and not raw:
         from .fp8_rows import dequantize_rows
         ori_rows, cmp_rows = dequantize_rows(ori_rows), dequantize_rows(cmp_rows)
     return ori_rows, cmp_rows
@@ -270,7 +329,8 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
                        ori_win_right: int = 0, layout_q: str = "TND",
                        head_dim_v: Optional[int] = None,
                        tokens: Optional[Sequence[int]] = None,
-                       kv_cache_dtype: Optional[str] = None, attend=None):
+                       kv_cache_dtype: Optional[str] = None, attend=None,
+                       fp8_qk: bool = False):
     """Golden output of ``sparse_attn_sharedkv`` for the API's own tensors.
 
     Returns ``(out, lse)`` in the caller's layout (``[T, N1, Dv]``/``[T, N1]``
@@ -278,9 +338,14 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
     stay zero (golden.py:106-111). ``tokens`` restricts the work to a subset
     of flat token ids (others stay zero) so large workloads can be sampled.
     ``attend`` replaces the per-token math (default ``attend_token``; the
-    kernel-order restatement of ``kernel_order`` plugs in here). All tensors
-    are read on the CPU.
+    kernel-order restatement of ``kernel_order`` plugs in here). ``fp8_qk``
+    (fp8 pools): the fp8 Q·Kᵀ form, ``attend_token_fp8qk`` on the raw rows.
+    All tensors are read on the CPU.
     """
+    if fp8_qk:
+        if not _is_fp8_pool(ori_kv, kv_cache_dtype):
+            raise ValueError("fp8_qk needs an fp8 pool")
+        attend = attend_token_fp8qk
     attend = attend_token if attend is None else attend
     q = q.cpu()
     n1, d = q.shape[-2], q.shape[-1]
@@ -311,7 +376,7 @@ def sparse_attn_oracle(q: torch.Tensor, *, ori_kv: torch.Tensor, ori_block_table
                 cmp_block_table=cmp_block_table,
                 cmp_idx_row=None if idx_flat is None else idx_flat[t, 0].tolist(),
                 cmp_ratio=cmp_ratio, ori_win_left=ori_win_left, ori_win_right=ori_win_right,
-                kv_cache_dtype=kv_cache_dtype)
+                kv_cache_dtype=kv_cache_dtype, raw=fp8_qk)
             o, l = attend(q_flat[t], [ori_rows, cmp_rows], sinks, softmax_scale, d_v=dv)
             out[t] = o
             lse[t] = l

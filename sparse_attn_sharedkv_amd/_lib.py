@@ -34,6 +34,7 @@ KV_NATIVE = 0
 KV_FP8_DS_MLA = 1
 FP8_ROW_BYTES = 656
 SAS_PHASE_PIPELINED = 4        # SasAttnArgs.phases bit: native rows through the pipelined kernel
+SAS_PHASE_FP8_QK = 8           # SasAttnArgs.phases bit: fp8 rows, Q·Kᵀ on fp8 MFMA (e4m3 queries)
 SCHED_DEVICE = -1             # SasAttnArgs.num_fd: schedule summary read on the device
 DEV_SCHED_MAX_BATCH = 4096
 DEV_SCHED_MAX_ITEMS = 16384

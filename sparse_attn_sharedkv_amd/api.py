@@ -72,6 +72,7 @@ class Prepared:
     layout_q: str = "TND"
     bsnd_shape: Optional[tuple] = None
     device: Optional[torch.device] = None
+    phase_bits: int = 0    # kernel-form bits every launch of this call carries (SAS_PHASE_FP8_QK)
 
 
 @functools.lru_cache(maxsize=64)
@@ -118,6 +119,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             head_dim_v: Optional[int] = None,
             kv_cache_dtype: Optional[str] = None,
             schedule: Optional[str] = None,
+            fp8_qk: bool = False,
             _stream_schedule: bool = False) -> Prepared:
     """Validate and stage one call (host work of api.py:186-384) without launching.
 
@@ -220,6 +222,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                                  f"[blocks, block_size, 1, {_lib.FP8_ROW_BYTES}]")
     elif ori_kv.dtype != dtype or (cmp_kv is not None and cmp_kv.dtype != dtype):
         raise ValueError("KV caches must have q's dtype")
+    if fp8_qk and not fp8:
+        raise ValueError("fp8_qk needs fp8_ds_mla cache rows")
     if ori_win_left < -1:
         raise ValueError("ori_win_left must be >= -1")
     if scenario >= 2:
@@ -340,7 +344,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             sinks_d, metadata_dev, out, lse, ws]
     return Prepared(args=a, keep=keep, out=out, lse=lse, layout_q=layout_q,
                     bsnd_shape=None if layout_q == "TND" else (nb, total // max(nb, 1), n1, dv),
-                    device=dev)
+                    device=dev, phase_bits=_lib.SAS_PHASE_FP8_QK if fp8_qk else 0)
 
 
 def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: int = 0) -> None:
@@ -351,7 +355,7 @@ def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: i
     """
     lib = _lib.load()
     st = stream if stream is not None else torch.cuda.current_stream(prep.device)
-    prep.args.phases = int(phases)
+    prep.args.phases = int(phases) | prep.phase_bits
     rc = lib.sas_attention_launch(ctypes.byref(prep.args), ctypes.c_void_p(st.cuda_stream))
     if rc != _lib.SAS_OK:
         raise RuntimeError(_lib.last_error())
@@ -396,6 +400,7 @@ def sparse_attn_sharedkv(
     head_dim_v: Optional[int] = None,
     kv_cache_dtype: Optional[str] = None,
     schedule: Optional[str] = None,
+    fp8_qk: bool = False,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Sparse shared-KV attention forward; returns ``attention_out`` in q's layout.
 
@@ -406,6 +411,11 @@ def sparse_attn_sharedkv(
     built here from the inputs (api.py:335-360). ``schedule="device"`` builds it
     on the GPU instead, so the call never waits for the device (see ``prepare``);
     a ``metadata`` tensor on the GPU is used without being read back.
+    ``fp8_qk=True`` (fp8 caches only; no reference counterpart) forms Q·Kᵀ on fp8
+    MFMA with each head's query latent quantized to e4m3 (one fp32 scale per
+    head); P·V stays bf16. It adds the query's quantization error: within
+    atol = rtol = 2e-2 of golden on N(0, 1)-scaled data, not on the reference
+    tests' U(-10, 10) data.
     """
     prep = prepare(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
                    ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
@@ -415,6 +425,7 @@ def sparse_attn_sharedkv(
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
                    core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
-                   kv_cache_dtype=kv_cache_dtype, schedule=schedule, _stream_schedule=True)
+                   kv_cache_dtype=kv_cache_dtype, schedule=schedule, fp8_qk=fp8_qk,
+                   _stream_schedule=True)
     launch(prep)
     return finalize(prep, return_softmax_lse)

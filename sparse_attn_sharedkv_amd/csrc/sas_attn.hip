@@ -58,6 +58,8 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 #define SAS_LDS __attribute__((address_space(3)))
 #define SAS_GLOBAL __attribute__((address_space(1)))
@@ -169,6 +171,46 @@ __device__ inline void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// N dword loads and their vmcnt(0) wait in ONE asm statement. Loads issued by
+// separate asm statements leave the compiler free to place code between a load
+// and its wait; under register pressure that code can spill the destination
+// register (storing its stale value) and reuse it, and the load then lands in a
+// register that holds something else by then (an address, which faulted the GPU).
+// Early-clobber outputs keep the destinations apart from the address operands.
+template <int N>
+__device__ inline void gather_dwords_wait(int (&v)[N], const int32_t* const (&p)[N]) {
+  static_assert(N == 6 || N == 8, "gather_dwords_wait: 6 or 8 loads");
+  if constexpr (N == 6) {
+    asm volatile(
+        "global_load_dword %0, %6, off\n\t"
+        "global_load_dword %1, %7, off\n\t"
+        "global_load_dword %2, %8, off\n\t"
+        "global_load_dword %3, %9, off\n\t"
+        "global_load_dword %4, %10, off\n\t"
+        "global_load_dword %5, %11, off\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
+        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5])
+        : "memory");
+  } else {
+    asm volatile(
+        "global_load_dword %0, %8, off\n\t"
+        "global_load_dword %1, %9, off\n\t"
+        "global_load_dword %2, %10, off\n\t"
+        "global_load_dword %3, %11, off\n\t"
+        "global_load_dword %4, %12, off\n\t"
+        "global_load_dword %5, %13, off\n\t"
+        "global_load_dword %6, %14, off\n\t"
+        "global_load_dword %7, %15, off\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7])
+        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]),
+          "v"(p[7])
+        : "memory");
+  }
+}
+
 // Cache rows that a tile holds but the softmax masks (tile tails, -1 and
 // out-of-range top-k ids) are read from this all-zero row instead of the
 // pool: their P is 0, and 0 * V is only 0 when V is finite, which an
@@ -232,6 +274,50 @@ __device__ inline i16x8 fp8x8_dequant_bf16(uint2 v, float s) {
   const s2 w0 = __builtin_bit_cast(s2, b0), w1 = __builtin_bit_cast(s2, b1);
   const s2 w2 = __builtin_bit_cast(s2, b2), w3 = __builtin_bit_cast(s2, b3);
   return (i16x8){w0[0], w0[1], w1[0], w1[1], w2[0], w2[1], w3[0], w3[1]};
+}
+
+// fp8 Q·Kᵀ: a head's 512 latent query dims as e4m3 codes of q * (448 / amax)
+// (one IEEE fp32 division per head, then an fp32 product per dim, clamped to ±448
+// and rounded to nearest even by v_cvt_pk_fp8_f32), with sq = amax / 448 the
+// factor that scales the scores back (both 1 for an all-zero head). The lane holds dims
+// 128 blk + 32 g4 + 8 h + e of its head in qf[4 blk + h][e] (bf16 bits); the
+// head's other dims sit in lanes l ^ 16, l ^ 32, l ^ 48. q8[blk] is the 16x16x128
+// B operand of block blk: byte p = dim 128 blk + 32 g4 + p.
+__device__ inline void quantize_q(const i16x8 (&qf)[18], i32x8 (&q8)[4], float& sq) {
+  auto f32 = [](short v) { return __uint_as_float((uint32_t)(uint16_t)v << 16); };
+  // amax on the bf16 bits (|x| orders as its low 15 bits), one k-step at a time:
+  // fp32 conversions here would be kept for the quantization below, and the
+  // scheduler would convert every dim at once, more than the registers of the
+  // loop around this can hold
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 mb = {0, 0};
+#pragma unroll
+  for (int ks = 0; ks < 16; ++ks) {
+    const i32x4 wv = __builtin_bit_cast(i32x4, qf[ks]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      mb = __builtin_elementwise_max(mb, __builtin_bit_cast(u16x2, wv[e] & 0x7FFF7FFF));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float amax = __uint_as_float((uint32_t)(mb[0] > mb[1] ? mb[0] : mb[1]) << 16);
+  const auto r1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(amax), __float_as_uint(amax),
+                                                   false, false);
+  amax = wave_max_pair(fmaxf(__uint_as_float(r1[0]), __uint_as_float(r1[1])));
+  sq = amax > 0.0f ? amax / 448.0f : 1.0f;
+  const float inv = amax > 0.0f ? 448.0f / amax : 1.0f;
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const i16x8 v = qf[4 * blk + (d >> 1)];
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(f32(v[4 * (d & 1) + i]) * inv, -448.0f), 448.0f);
+      int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+      w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
+      q8[blk][d] = w;
+      __builtin_amdgcn_sched_barrier(0);  // (one word at a time, as above)
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -505,26 +591,26 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
       auto extra_slot = [&](int x) { return x < own_lo ? x : x + (own_hi - own_lo); };
       int sv0[SCAN_PER];
       if (scan3) {
-        // all loads issued, then one wait that also ties their destinations
+        // all loads issued and waited for in one asm statement (gather_dwords_wait)
         int v[PER];
+        const int32_t* src[PER + SCAN_PER];
+        int got[PER + SCAN_PER];
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
           const int jj = c0 + e * NT + tid - g.n_win;
-          const int32_t* src = idx_row + (jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1));
-          asm volatile("global_load_dword %0, %1, off" : "=v"(v[e]) : "v"(src) : "memory");
+          src[e] = idx_row + (jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1));
         }
 #pragma unroll
         for (int e = 0; e < SCAN_PER; ++e) {
           const int x = e * NT + tid;  // clamped into range; unused when n_extra == 0
           const int xc = x < n_extra ? x : (n_extra > 0 ? n_extra - 1 : 0);
-          const int32_t* src = idx_row + (n_extra > 0 ? extra_slot(xc) : 0);
-          asm volatile("global_load_dword %0, %1, off" : "=v"(sv0[e]) : "v"(src) : "memory");
+          src[PER + e] = idx_row + (n_extra > 0 ? extra_slot(xc) : 0);
         }
-        asm volatile("s_waitcnt vmcnt(0)"
-                     : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(sv0[0]),
-                       "+v"(sv0[1]), "+v"(sv0[2]), "+v"(sv0[3])
-                     :
-                     : "memory");
+        gather_dwords_wait(got, src);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) v[e] = got[e];
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) sv0[e] = got[PER + e];
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
           const int r = e * NT + tid;
@@ -1048,7 +1134,7 @@ __device__ __host__ inline int ring_row_base(int r) {
 }
 __device__ __host__ inline int ring_rope_slot(int r, int c) { return 8 * r + (c ^ ((r >> 1) & 7)); }
 
-template <int DQK, int DV, int NHG, typename T, int KVF>
+template <int DQK, int DV, int NHG, typename T, int KVF, bool QK8 = false>
 __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   constexpr int NW = 4 * NHG;            // waves per workgroup
   constexpr int MB = 32 * NHG;           // heads per item (m-block)
@@ -1061,9 +1147,19 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   constexpr int NKS_MAIN = 16;           // k-steps over the 512 main dims
   constexpr int DVQ = DV / 4;            // dv per wave (a quarter)
   constexpr int DVB = DVQ / 32;          // 32-wide dv blocks per wave (4)
-  constexpr int NSTG = 4;                // LDS ring depth
+  // LDS ring depth: the DMA path keeps tile it + 3 in flight; fp8 rows fill tile
+  // it + 2 from registers, which three stages hold (the fp8 Q·Kᵀ form needs the
+  // space of the fourth for its e4m3 K stages)
+  constexpr int NSTG = QK8 ? 3 : 4;
   constexpr int STAGE_BYTES = MAIN_BYTES + (ROPE ? ROPE_BYTES : 0);
   constexpr int PB_HG = 32 * 64;         // Pᵀ of one head group: 32 heads x 32 rows x 2 B
+  // fp8 Q·Kᵀ (QK8): two stages of the tile's raw e4m3 dims 0..511 (row r at
+  // r * K8_ROW: the 528-byte stride puts the 16 rows of a K-operand read in 16
+  // distinct bank groups) followed by the block scales as [block][row] floats
+  constexpr int K8_ROW = 528;
+  constexpr int K8_SCALES = TILE * K8_ROW;
+  constexpr int K8_STAGE = K8_SCALES + 4 * TILE * 4;
+  constexpr int K8_BASE = NSTG * STAGE_BYTES + (ROPE ? 0 : NHG * PB_HG);
   constexpr int ROWS_PER_WAVE = TILE / NW;             // main-part DMA instructions per wave
   constexpr int NROPE = ROPE ? TILE / 8 : 0;           // rope DMA instructions per tile (4)
   constexpr int DMA_MAX = ROWS_PER_WAVE + (ROPE ? 1 : 0);  // per wave and tile (waves w < NROPE)
@@ -1074,13 +1170,13 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   static_assert(TILE % NW == 0 && NROPE <= NW, "DMA split");
   static_assert(!ROPE || NHG * PB_HG <= ROPE_BYTES, "Pᵀ in the rope part of a stage");
   static_assert(!FP8 || (ROPE && __is_same(T, __bf16)), "fp8 rows: head_dim 576, bf16");
+  static_assert(!QK8 || FP8, "fp8 Q·Kᵀ reads fp8 rows");
   constexpr int RPL = 2 * ROWS_PER_WAVE;  // fp8 rows: rope bytes per lane per tile (8 or 16)
   typedef uint32_t ropev __attribute__((ext_vector_type(RPL / 4)));
   typedef MfmaOps<T> Ops;
   typedef typename Ops::vec8 vec8;
 
-  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTG * STAGE_BYTES +
-                                                                 (ROPE ? 0 : NHG * PB_HG)];
+  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[K8_BASE + (QK8 ? 2 * K8_STAGE : 0)];
   __shared__ float htab[NHG][32];     // per head: rescale factor of the tile / final m
   __shared__ float xmax[NHG][2][32];  // per head and row half: row max of a tile / final l
   __shared__ uint32_t rowid[RCH];
@@ -1205,6 +1301,10 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
 
     // query fragment of the wave's 16 heads (B operand of Sᵀ = K·Qᵀ)
     i16x8 qf[NKS];
+    // fp8 Q·Kᵀ: the head's latent as e4m3 codes of q / sq (B operands of the four
+    // 128-dim blocks), sq = amax / 448 over the head's 512 latent dims
+    i32x8 q8[4];
+    float sq = 1.0f;
     // ---- online-softmax state of head hq (golden.py:156-160 seeds m = sink,
     // l = 1; the 1 goes to the lanes of group 0 of the first row half, whose row
     // sums are added to the others' at the end) ----
@@ -1250,7 +1350,11 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
                                                  (hok ? head_q : 0)) * DQK;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-          i16x8 v = *(const i16x8*)(qrow + 32 * ks + 8 * g4);
+          // (fp8 Q·Kᵀ: latent k-step 4 blk + h holds dims 128 blk + 32 g4 + 8 h, the
+          // lane's quarter of e4m3 block blk)
+          const int dim = (QK8 && ks < NKS_MAIN) ? 128 * (ks >> 2) + 32 * g4 + 8 * (ks & 3)
+                                                 : 32 * ks + 8 * g4;
+          i16x8 v = *(const i16x8*)(qrow + dim);
           qf[ks] = hok ? v : (i16x8){0, 0, 0, 0, 0, 0, 0, 0};
         }
       }
@@ -1266,34 +1370,26 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       auto extra_slot = [&](int x) { return x < own_lo ? x : x + (own_hi - own_lo); };
       int sv0[SCAN_PER];
       if (scan3) {
-        // all loads issued, then one wait that also ties their destinations
+        // all loads issued and waited for in one asm statement (gather_dwords_wait)
         int v[PER];
+        const int32_t* src[PER + SCAN_PER];
+        int got[PER + SCAN_PER];
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
           const int jj = c0 + e * NT + tid - g.n_win;
-          const int32_t* src = idx_row + (jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1));
-          asm volatile("global_load_dword %0, %1, off" : "=v"(v[e]) : "v"(src) : "memory");
+          src[e] = idx_row + (jj < 0 ? 0 : (jj < a.topk ? jj : a.topk - 1));
         }
 #pragma unroll
         for (int e = 0; e < SCAN_PER; ++e) {
           const int x = e * NT + tid;  // clamped into range; unused when n_extra == 0
           const int xc = x < n_extra ? x : (n_extra > 0 ? n_extra - 1 : 0);
-          const int32_t* src = idx_row + (n_extra > 0 ? extra_slot(xc) : 0);
-          asm volatile("global_load_dword %0, %1, off" : "=v"(sv0[e]) : "v"(src) : "memory");
+          src[PER + e] = idx_row + (n_extra > 0 ? extra_slot(xc) : 0);
         }
-        if constexpr (PER == 4) {
-          asm volatile("s_waitcnt vmcnt(0)"
-                       : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(sv0[0]),
-                         "+v"(sv0[1]), "+v"(sv0[2]), "+v"(sv0[3])
-                       :
-                       : "memory");
-        } else {
-          asm volatile("s_waitcnt vmcnt(0)"
-                       : "+v"(v[0]), "+v"(v[1]), "+v"(sv0[0]), "+v"(sv0[1]), "+v"(sv0[2]),
-                         "+v"(sv0[3])
-                       :
-                       : "memory");
-        }
+        gather_dwords_wait(got, src);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) v[e] = got[e];
+#pragma unroll
+        for (int e = 0; e < SCAN_PER; ++e) sv0[e] = got[PER + e];
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
           const int r = e * NT + tid;
@@ -1353,6 +1449,9 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       // every load so far (table words, query fragment) has landed, as the compiler sees it
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
       if (c0 == p_lo) m_run = seed_m();
+      if constexpr (QK8) {
+        if (c0 == p_lo) quantize_q(qf, q8, sq);
+      }
       if (stop_pending) {
         __syncthreads();  // every thread's atomicMin is in
         cmp_stop = min(first_neg[item_par], g.n_cmp);
@@ -1480,6 +1579,16 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
           const int r = w + NW * j;
           *(i16x8*)(sb + ring_row_base(r) + 16 * lane) = fp8x8_dequant_bf16(f.v[j], f.s[j]);
         }
+        if constexpr (QK8) {
+          // the raw e4m3 bytes and the block scales into the tile's K8 stage
+          unsigned char* kb8 = kv_lds + K8_BASE + (tile & 1) * K8_STAGE;
+#pragma unroll
+          for (int j = 0; j < ROWS_PER_WAVE; ++j) {
+            const int r = w + NW * j;
+            *(uint2*)(kb8 + r * K8_ROW + 8 * lane) = f.v[j];
+            if ((lane & 15) == 0) *(float*)(kb8 + K8_SCALES + 4 * ((lane >> 4) * TILE + r)) = f.s[j];
+          }
+        }
         // the lane's RPL rope bytes: whole 16-byte chunks (RPL 16; consecutive chunks
         // of a row need not be adjacent in the rotated rope layout, so one store
         // each) or half of one (RPL 8)
@@ -1512,6 +1621,39 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
         const lds_p p = ks < NKS_MAIN ? sb + k_base + 64 * ks
                                       : sb + (ks == NKS_MAIN ? rope_k0 : rope_k1);
         return *(const i16x8 SAS_LDS*)p;
+      };
+      // fp8 Q·Kᵀ: the e4m3 A operand of block blk (the wave's row k_row, bytes
+      // 128 blk + 32 g4 .. + 31) from a K8 stage, and the scores of the wave's 16
+      // rows x 16 heads from the four blocks' dot products d8, the rope part dr and
+      // the row scales: s = sq * sum_blk sk[blk][row] * d8[blk] + dr
+      auto k8_stage = [&](int tile) -> lds_p {
+        return (lds_p)(kv_base + (uint32_t)(K8_BASE + (tile & 1) * K8_STAGE));
+      };
+      auto k8op = [&](lds_p kb8, int blk) -> i32x8 {
+        const lds_p p = kb8 + k_row * K8_ROW + 128 * blk + 32 * g4;
+        const i32x4 lo = *(const i32x4 SAS_LDS*)p;
+        const i32x4 hi = *(const i32x4 SAS_LDS*)(p + 16);
+        return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      };
+      // block blk's scales of the wave's output rows 16 rh + 4 g4 + i (element i)
+      auto k8scale = [&](lds_p kb8, int blk) -> f32x4 {
+        return *(const f32x4 SAS_LDS*)(kb8 + K8_SCALES + 4 * (blk * TILE + 16 * rh + 4 * g4));
+      };
+      auto mma8 = [&](i32x8 x, i32x8 y) -> f32x4 {
+        // e4m3 x e4m3 (format selectors 0), no block scaling: v_mfma_f32_16x16x128_f8f6f4
+        return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, (f32x4){0.0f, 0.0f, 0.0f, 0.0f},
+                                                                0, 0, 0, 0, 0, 0);
+      };
+      // s8 (+)= d * sk, element-wise (block 0 starts the sum: s8 = d * sk)
+      auto scale_add = [&](f32x4& s8, f32x4 d, f32x4 sk, bool first) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s8[i] = first ? d[i] * sk[i] : __builtin_fmaf(d[i], sk[i], s8[i]);
+      };
+      auto scores8 = [&](f32x4 s8, f32x4 dr) -> f32x4 {
+        f32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = __builtin_fmaf(s8[i], sq, dr[i]);
+        return r;
       };
       auto mma16 = [&](i16x8 x, i16x8 y, f32x4 c) -> f32x4 {
         return __is_same(T, __bf16)
@@ -1559,12 +1701,23 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       {
         const lds_p sb = stage_of(0);
         f32x4 ce = {0.0f, 0.0f, 0.0f, 0.0f}, co = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (QK8) {
+          const lds_p kb8 = k8_stage(0);
+          f32x4 s8 = ce;
 #pragma unroll
-        for (int ks = 0; ks < NKS; ks += 2) {
-          ce = mma16(kop(sb, ks), qf[ks], ce);
-          co = mma16(kop(sb, ks + 1), qf[ks + 1], co);
+          for (int blk = 0; blk < 4; ++blk)
+            scale_add(s8, mma8(k8op(kb8, blk), q8[blk]), k8scale(kb8, blk), blk == 0);
+          ce = mma16(kop(sb, NKS_MAIN), qf[NKS_MAIN], ce);
+          ce = mma16(kop(sb, NKS_MAIN + 1), qf[NKS_MAIN + 1], ce);
+          st = scores8(s8, ce);
+        } else {
+#pragma unroll
+          for (int ks = 0; ks < NKS; ks += 2) {
+            ce = mma16(kop(sb, ks), qf[ks], ce);
+            co = mma16(kop(sb, ks + 1), qf[ks + 1], co);
+          }
+          st = ce + co;
         }
-        st = ce + co;
         const float own = row_max(st, 0);
         __syncthreads();
         mx = fmaxf(own, xmax[hg][rh ^ 1][16 * qh + r16]);
@@ -1584,11 +1737,18 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
         float own = -INFINITY;
         auto phase_a = [&](auto with_qk) {
           constexpr bool QK = decltype(with_qk)::value;
-          constexpr int KPF = FP8 ? 3 : 6;
+          constexpr int KPF = QK8 ? 1 : FP8 ? 3 : 6;
           const lds_p sbn = stage_of(it + 1);
           i16x8 kb[KPF];
           f32x4 ce = {0.0f, 0.0f, 0.0f, 0.0f}, co = {0.0f, 0.0f, 0.0f, 0.0f};
-          if constexpr (QK) {
+          // fp8 Q·Kᵀ: the e4m3 A operands two blocks ahead, the row scales
+          const lds_p kb8n = QK8 ? k8_stage(it + 1) : sbn;
+          i32x8 k8b[2];
+          f32x4 s8, d8, skb;  // running block sum, last block's product and scales
+          if constexpr (QK && QK8) {
+            k8b[0] = k8op(kb8n, 0);
+            k8b[1] = k8op(kb8n, 1);
+          } else if constexpr (QK) {
 #pragma unroll
             for (int i = 0; i < KPF; ++i) kb[i] = kop(sbn, i);
           }
@@ -1624,10 +1784,29 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
             }
           };
           constexpr int DMA_AT = 6;  // first k-step with a DMA after it
-          constexpr int NSTEP = NKS > DMA_AT + DMA_MAX ? NKS : DMA_AT + DMA_MAX;
+          // fp8 Q·Kᵀ: steps 0..3 are the e4m3 blocks, 4 and 5 the rope k-steps
+          constexpr int NSTEP = QK8 ? 6 : NKS > DMA_AT + DMA_MAX ? NKS : DMA_AT + DMA_MAX;
 #pragma unroll
           for (int ks = 0; ks < NSTEP; ++ks) {
-            if constexpr (QK) {
+            if constexpr (QK && QK8) {
+              // step k: block k's MFMA, then block k - 1's product scaled into the sum
+              // (its MFMA has drained under block k's)
+              if (ks < 4) {
+                const f32x4 dn = mma8(k8b[ks & 1], q8[ks]);
+                if (ks + 2 < 4) k8b[ks & 1] = k8op(kb8n, ks + 2);
+                if (ks > 0) scale_add(s8, d8, skb, ks == 1);
+                d8 = dn;
+                skb = k8scale(kb8n, ks);
+                if (ks == 3) kb[0] = kop(sbn, NKS_MAIN);
+              } else {
+                const i16x8 k0 = kb[0];
+                if (ks == 4) {
+                  kb[0] = kop(sbn, NKS_MAIN + 1);
+                  scale_add(s8, d8, skb, false);
+                }
+                ce = mma16(k0, qf[NKS_MAIN + ks - 4], ce);
+              }
+            } else if constexpr (QK) {
               if (ks < NKS) {
                 const i16x8 k0 = kb[ks % KPF];
                 if (ks + KPF < NKS) kb[ks % KPF] = kop(sbn, ks + KPF);
@@ -1645,7 +1824,8 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
             __builtin_amdgcn_sched_barrier(0);
           }
           if constexpr (QK) {
-            sn = ce + co;
+            if constexpr (QK8) sn = scores8(s8, ce);
+            else sn = ce + co;
             own = row_max(sn, it + 1);
           }
         };
@@ -1997,8 +2177,12 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     // native rows: one wave per SIMD (attn2_kernel); fp8 rows: the pipelined
     // two-waves-per-SIMD kernel, whose second wave hides the dequantization
     if constexpr (KVF == SAS_KV_FP8_DS_MLA) {
-      hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
-                         dim3(256 * NHG), 0, st, a);
+      if (a.phases & SAS_PHASE_FP8_QK)
+        hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF, true>), dim3(8 * per_xcd),
+                           dim3(256 * NHG), 0, st, a);
+      else
+        hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
+                           dim3(256 * NHG), 0, st, a);
     } else {
       if (a.phases & SAS_PHASE_PIPELINED)
         hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
@@ -2077,8 +2261,12 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     set_error("sas_attention_launch: scenario inputs missing");
     return SAS_E_INVALID;
   }
-  if (a->phases < 0 || a->phases > 7) {
-    set_error("sas_attention_launch: phases must be 0..7");
+  if (a->phases < 0 || a->phases > 15) {
+    set_error("sas_attention_launch: phases must be 0..15");
+    return SAS_E_INVALID;
+  }
+  if ((a->phases & SAS_PHASE_FP8_QK) && a->kv_format != SAS_KV_FP8_DS_MLA) {
+    set_error("sas_attention_launch: SAS_PHASE_FP8_QK needs fp8 cache rows (SAS_KV_FP8_DS_MLA)");
     return SAS_E_INVALID;
   }
   const bool dev_sched = a->num_fd == SAS_SCHED_DEVICE;
@@ -2181,7 +2369,7 @@ extern "C" int sas_attention_launch_noalloc(const SasAttnArgs* a, void* stream) 
   return sas_attention_launch(&b, stream);
 }
 
-extern "C" int sas_version(void) { return 110; }
+extern "C" int sas_version(void) { return 111; }
 
 extern "C" int sas_args_struct_size(void) { return (int)sizeof(SasAttnArgs); }
 

@@ -43,8 +43,12 @@ def sparse_flash_mla(
     head_dim_v: Optional[int] = 512,
     kv_cache_dtype: Optional[str] = None,
     schedule: Optional[str] = None,
+    fp8_qk: bool = False,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
-    """Sparse flash-MLA forward: ``attention_out`` (and lse) in q's layout."""
+    """Sparse flash-MLA forward: ``attention_out`` (and lse) in q's layout.
+
+    ``fp8_qk``: as in ``sparse_attn_sharedkv`` (fp8 caches: Q·Kᵀ on fp8 MFMA).
+    """
     prep = prepare(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
                    ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
                    cu_seqlens_q=cu_seqlens_q, seqused_q=seqused_q, seqused_kv=seqused_kv,
@@ -53,6 +57,7 @@ def sparse_flash_mla(
                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
                    core_num=core_num, topk_cmp=topk_cmp, head_dim_v=head_dim_v,
-                   kv_cache_dtype=kv_cache_dtype, schedule=schedule, _stream_schedule=True)
+                   kv_cache_dtype=kv_cache_dtype, schedule=schedule, fp8_qk=fp8_qk,
+                   _stream_schedule=True)
     launch(prep)
     return finalize(prep, return_softmax_lse)

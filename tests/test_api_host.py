@@ -118,3 +118,9 @@ def test_short_length_and_table_tensors(swa_case, scfa_case):
     with pytest.raises(ValueError):
         sparse_attn_sharedkv(**dict(scfa_case,
                                     cmp_block_table=scfa_case["cmp_block_table"][: nb - 1]))
+
+
+def test_fp8_qk_needs_fp8_rows(swa_case):
+    # the fp8 Q·Kᵀ form reads e4m3 cache rows: on native rows it is a ValueError
+    with pytest.raises(ValueError, match="fp8_qk"):
+        sparse_attn_sharedkv(**dict(swa_case), fp8_qk=True)

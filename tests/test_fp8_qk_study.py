@@ -14,17 +14,54 @@ import numpy as np
 import torch
 
 from oracle import fp8_qk_study as st
-from oracle.fp8_rows import E4M3_MAX, decode_e4m3, quantize_rows
+from oracle.fp8_rows import E4M3_MAX, decode_e4m3, quantize_q, quantize_rows, scores_fp8
 
 
 def test_query_quantizer_matches_torch_cast():
     g = torch.Generator().manual_seed(1)
     q = (torch.randn(16, 576, generator=g) * 3).to(torch.bfloat16).float().numpy()
-    codes, sq = st.quantize_q(q)
-    ref = torch.from_numpy(q[:, :512] / sq[:, None]).to(torch.float8_e4m3fn)
+    q[3] = 0.0                                   # an all-zero head: codes 0, sq 1
+    codes, sq = quantize_q(q)
+    amax = np.abs(q[:, :512]).max(axis=1)
+    inv = np.where(amax > 0, np.float32(448) / np.where(amax > 0, amax, 1), 1).astype(np.float32)
+    x = torch.from_numpy((q[:, :512] * inv[:, None]).astype(np.float32)).clamp(-448, 448)
+    ref = x.to(torch.float8_e4m3fn)
     assert np.array_equal(codes, ref.view(torch.uint8).numpy())
+    assert sq[3] == 1.0 and not codes[3].any()
     # each head's largest |latent| maps to +-448 exactly
-    assert np.allclose(np.abs(decode_e4m3(codes)).max(axis=1), E4M3_MAX)
+    nz = amax > 0
+    assert np.allclose(np.abs(decode_e4m3(codes[nz])).max(axis=1), E4M3_MAX)
+    assert np.array_equal(sq[nz], (amax[nz] / np.float32(448)).astype(np.float32))
+
+
+def test_fp8_scores_exact_on_exactly_representable_operands():
+    """Power-of-two block scales and queries that are e4m3 values times a power of
+    two: quantization and dequantization are exact, so the fp8 scores equal
+    golden's scores on the dequantized bf16 rows (a wrong block, scale or row index
+    changes them)."""
+    g = torch.Generator().manual_seed(5)
+    n, heads = 40, 6
+    codes = torch.randint(0, 0x7E, (n, 512), generator=g).numpy().astype(np.uint8)
+    codes |= (torch.rand(n, 512, generator=g).numpy() < 0.5).astype(np.uint8) << 7
+    raw = np.zeros((n, 656), dtype=np.uint8)
+    raw[:, :512] = codes
+    sc = np.float32(2.0) ** torch.randint(-6, 3, (n, 4), generator=g).numpy().astype(np.float32)
+    raw[:, 512:528] = sc.astype("<f4").view(np.uint8).reshape(n, 16)
+    rope = (torch.randn(n, 64, generator=g) * 0.5).to(torch.bfloat16)
+    raw[:, 528:] = rope.view(torch.int16).numpy().astype("<i2").view(np.uint8).reshape(n, 128)
+    qc = torch.randint(0, 0x7E, (heads, 512), generator=g).numpy().astype(np.uint8)
+    qc[:, 0] = 0x7E                              # amax = 448 * 2^e exactly
+    qv = decode_e4m3(qc) * np.float32(2.0) ** np.arange(-2, heads - 2, dtype=np.float32)[:, None]
+    q = np.concatenate([qv, (torch.randn(heads, 64, generator=g) * 0.5).to(torch.bfloat16)
+                        .float().numpy()], axis=1).astype(np.float32)
+    k = st.dequant_bf16(raw).astype(np.float64)
+    scale = 1 / math.sqrt(576)
+    expect = ((q.astype(np.float64) @ k.T) * scale).astype(np.float32)
+    assert np.array_equal(scores_fp8(q, raw, scale), expect)
+    # block 1's scales replaced by 1.0: visible in the scores
+    raw2 = raw.copy()
+    raw2[:, 516:520] = np.frombuffer(np.full(n, 1.0, "<f4").tobytes(), np.uint8).reshape(n, 4)
+    assert not np.array_equal(scores_fp8(q, raw2, scale), expect)
 
 
 def test_fp8_scores_equal_the_product_of_the_dequantized_operands():
@@ -32,7 +69,7 @@ def test_fp8_scores_equal_the_product_of_the_dequantized_operands():
     kv = (torch.randn(64, 576, generator=g) * 0.7).to(torch.bfloat16)
     raw = quantize_rows(kv)
     q = (torch.randn(8, 576, generator=g)).to(torch.bfloat16).float().numpy()
-    codes, sq = st.quantize_q(q)
+    codes, sq = quantize_q(q)
     q_deq = np.concatenate([decode_e4m3(codes).astype(np.float64) * sq[:, None].astype(np.float64),
                             q[:, 512:].astype(np.float64)], axis=1)
     k8 = decode_e4m3(raw[:, :512]).astype(np.float64).reshape(-1, 4, 128)
@@ -42,7 +79,7 @@ def test_fp8_scores_equal_the_product_of_the_dequantized_operands():
     k_deq = np.concatenate([(k8 * sk[:, :, None]).reshape(-1, 512), rope], axis=1)
     scale = 1 / math.sqrt(576)
     expect = (q_deq @ k_deq.T) * scale
-    got = st.scores_fp8(q, raw, scale).astype(np.float64)
+    got = scores_fp8(q, raw, scale).astype(np.float64)
     assert np.allclose(got, expect, rtol=1e-5, atol=1e-6)
 
 
@@ -52,3 +89,39 @@ def test_benchmark_data_within_the_bound_reference_data_not():
     assert normal["lse_max_rel"] < 1e-3, normal
     uniform = st.run("uniform", tokens=1, heads=64, rows=1024, seed=3)
     assert uniform["beyond_frac"] > 0.01 and uniform["lse_max_rel"] > 1e-3, uniform
+
+
+def test_attend_on_scores_equals_golden_bitwise():
+    """``attend_token_scores`` fed golden's own scores is ``attend_token`` exactly
+    (tiles, sink seeding, P rounding and fp32 state are the same code path)."""
+    from oracle.golden_ref import attend_token, attend_token_scores
+    g = torch.Generator().manual_seed(11)
+    q = (torch.randn(8, 576, generator=g) * 0.5).to(torch.bfloat16)
+    segs = [(torch.randn(n, 576, generator=g) * 0.5).to(torch.bfloat16) for n in (130, 0, 700)]
+    sinks = torch.randn(8, generator=g)
+    scale = 1 / math.sqrt(576)
+    o_ref, l_ref = attend_token(q, segs, sinks, scale, d_v=512)
+    # golden's scores, formed tile by tile as attend_token forms them
+    sc = [torch.cat([(q.float() @ s[t:t + 512].float().T) * scale
+                     for t in range(0, s.shape[0], 512)] or [torch.zeros(8, 0)], dim=1)
+          for s in segs]
+    o, l = attend_token_scores(sc, [s[:, :512] for s in segs], sinks, q.dtype)
+    assert torch.equal(o, o_ref) and torch.equal(l, l_ref)
+
+
+def test_fp8qk_oracle_close_to_golden_on_benchmark_data():
+    """The fp8 Q·Kᵀ oracle on N(0, 1) * 0.5 data sits within the benchmark bound
+    of golden on the dequantized cache."""
+    from oracle.checks import check_strict
+    from oracle.golden_ref import attend_token, attend_token_fp8qk
+    from oracle.fp8_rows import dequantize_rows
+    g = torch.Generator().manual_seed(12)
+    q = (torch.randn(16, 576, generator=g) * 0.5).to(torch.bfloat16)
+    raws = [quantize_rows((torch.randn(n, 576, generator=g) * 0.5).to(torch.bfloat16))
+            for n in (128, 600)]
+    sinks = torch.randn(16, generator=g)
+    scale = 1 / math.sqrt(576)
+    o8, l8 = attend_token_fp8qk(q, [torch.from_numpy(r) for r in raws], sinks, scale)
+    o, l = attend_token(q, [dequantize_rows(r) for r in raws], sinks, scale, d_v=512)
+    check_strict(o8, o, l8, l)
+    assert not torch.equal(o8, o)   # the query quantization is visible

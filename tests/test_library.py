@@ -48,6 +48,8 @@ def test_header_constants_match_binding():
     assert int(consts["SAS_KV_NATIVE"]) == _lib.KV_NATIVE
     assert int(consts["SAS_KV_FP8_DS_MLA"]) == _lib.KV_FP8_DS_MLA
     assert int(consts["SAS_FP8_ROW_BYTES"]) == _lib.FP8_ROW_BYTES == 512 + 16 + 128
+    assert int(consts["SAS_PHASE_PIPELINED"]) == _lib.SAS_PHASE_PIPELINED
+    assert int(consts["SAS_PHASE_FP8_QK"]) == _lib.SAS_PHASE_FP8_QK
     assert int(consts["SAS_SCHED_DEVICE"].strip("()")) == _lib.SCHED_DEVICE
     assert int(consts["SAS_DEV_SCHED_MAX_BATCH"]) == _lib.DEV_SCHED_MAX_BATCH
     assert int(consts["SAS_DEV_SCHED_MAX_ITEMS"]) == _lib.DEV_SCHED_MAX_ITEMS
