@@ -10,7 +10,10 @@ block tables, top-k sets, q) rotate so the 256 MB Infinity Cache cannot hold
 the gathered rows between calls. Inputs are resident in HBM and the schedule
 is precomputed before the timed region.
 
-Other workloads (``--workload``): the MTP and fp8 long-context decode shapes,
+Other workloads (``--workload``): the MTP and fp8 long-context decode shapes
+(the fp8 one with bf16 queries on the dequantized rows by default, the faster
+form; ``--qk fp8`` runs its Q·Kᵀ on fp8 MFMA with e4m3 queries, as the
+configuration names it),
 and the reference's own 8K prefill test shapes (``swa_prefill_t8192_h64``,
 ``cfa_prefill_t8192_h64``, ``scfa_prefill_t8192_h64``: H=64, d=512, block 128),
 whose ``roofline`` counts q, out and the distinct cache rows once (the rows are
@@ -60,6 +63,10 @@ def parse():
     ap.add_argument("--workload", default="mla_decode_b64_h128_k2048")
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--qk", choices=("auto", "bf16", "fp8"), default="auto",
+                    help="Q·Kᵀ form over fp8 cache rows: fp8 MFMA with e4m3 queries (fp8) or "
+                         "bf16 MFMA on the dequantized rows (bf16); auto = bf16, the faster one "
+                         "(measured on MI355X at 128 sequences, H=128, top-k 2048)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the benchmark, run 5 plain device copies of MIB MiB (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -100,7 +107,7 @@ def profiled_counters(workload):
     return out
 
 
-def cpu_baseline(inputs, counts, max_tokens=64):
+def cpu_baseline(inputs, counts, max_tokens=64, fp8_qk=False):
     """Golden-faithful CPU restatement (oracle/) over the query rows of one input set.
 
     Times up to ``max_tokens`` rows (all of them for the benchmark workloads up to
@@ -108,7 +115,7 @@ def cpu_baseline(inputs, counts, max_tokens=64):
     """
     import torch
 
-    from oracle.golden_ref import attend_token, token_layout, token_rows
+    from oracle.golden_ref import attend_token, attend_token_fp8qk, token_layout, token_rows
     from sparse_attn_sharedkv_amd.workloads import flops_and_bytes
 
     threads = os.cpu_count() or 1
@@ -136,16 +143,17 @@ def cpu_baseline(inputs, counts, max_tokens=64):
                 cmp_block_table=kw["cmp_block_table"],
                 cmp_idx_row=None if idx_flat is None else idx_flat[t].tolist(),
                 cmp_ratio=kw["cmp_ratio"], ori_win_left=kw["ori_win_left"],
-                kv_cache_dtype=kw.get("kv_cache_dtype"))
-            attend_token(q_flat[t], [ori, cmp], kw["sinks"], kw["softmax_scale"],
-                         d_v=kw["head_dim_v"])
+                kv_cache_dtype=kw.get("kv_cache_dtype"), raw=fp8_qk)
+            (attend_token_fp8qk if fp8_qk else attend_token)(
+                q_flat[t], [ori, cmp], kw["sinks"], kw["softmax_scale"], d_v=kw["head_dim_v"])
             if rep == 0:
                 attended += ori.shape[0] + cmp.shape[0]
         times.append(time.perf_counter() - t0)
     sec = sorted(times)[1]
     flops, _ = flops_and_bytes(counts)
     share = attended / max(counts["rows"], 1)  # FLOP share of the sampled rows
-    fp8 = " (fp8 rows dequantized on the CPU)" if kw.get("kv_cache_dtype") else ""
+    fp8 = (" (fp8 rows: e4m3 Q·Kᵀ scores in float64, dequantized values)" if fp8_qk else
+           " (fp8 rows dequantized on the CPU)" if kw.get("kv_cache_dtype") else "")
     return {"value": round(flops * share / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port", "us_per_call": round(sec / share * 1e6, 1),
             "sample": f"{len(rows)} of {counts['tokens']} query rows of one input set, evenly "
@@ -174,10 +182,17 @@ def main():
     sets = [build_workload(args.workload, device=dev, seed=100 + i) for i in range(args.sets)]
     counts = workload_counts(sets[0])
     flops, nbytes = flops_and_bytes(counts)
+    fp8_rows = sets[0].get("kv_cache_dtype") is not None
+    fp8_qk = fp8_rows and args.qk == "fp8"
+    if args.qk == "fp8" and not fp8_rows:
+        print("--qk fp8 needs a workload with fp8 cache rows", file=sys.stderr)
+        sys.exit(2)
+    # committed profile summaries are named for the workload (and the Q·Kᵀ form)
+    prof_key = args.workload + ("_fp8qk" if fp8_qk else "")
     preps = []
     for kw in sets:
         call = {k: v for k, v in kw.items()}
-        preps.append(api.prepare(**call))
+        preps.append(api.prepare(**call, fp8_qk=fp8_qk))
     torch.cuda.synchronize()
 
     k, wu = args.steps, args.warmup
@@ -230,20 +245,20 @@ def main():
             ach = pbytes / (attn_avg * 1e-3) / 1e9
             roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                    "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(pbytes),
+                    "traffic": measured_traffic(prof_key), "algorithmic_bytes": int(pbytes),
                     "kernel": kernel}
         else:
             ach = flops / (attn_avg * 1e-3) / 1e12
             roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
-                    "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(pbytes),
+                    "traffic": measured_traffic(prof_key), "algorithmic_bytes": int(pbytes),
                     "kernel": kernel}
         roof["hbm_time_us"] = round(t_hbm * 1e6, 1)
         roof["mfma_time_us"] = round(t_mfma * 1e6, 1)
     else:
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                "traffic": measured_traffic(args.workload), "algorithmic_bytes": int(nbytes),
+                "traffic": measured_traffic(prof_key), "algorithmic_bytes": int(nbytes),
                 "kernel": kernel}
     res = {
         "metric": METRIC,
@@ -256,14 +271,17 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if sets[0].get("kv_cache_dtype") is None else "bf16 (fp8 e4m3 KV rows)",
+        "dtype": ("bf16" if not fp8_rows else
+                  "fp8 e4m3 Q·Kᵀ, bf16 P·V (fp8 e4m3 KV rows)" if fp8_qk else
+                  "bf16 (fp8 e4m3 KV rows)"),
         "data": "synthetic",
         "config": {"workload": args.workload, "batch": w["B"], "s_q": w["S"], "heads": w["H"],
                    "d_qk": w["D"], "d_v": w["DV"], "topk": w["K"], "ctx": list(w["ctx"]),
                    "block_size": w.get("block", 64), "input_sets": len(preps),
                    "tokens": counts["tokens"],
                    "attended_rows": counts["rows"], "layout_q": sets[0]["layout_q"],
-                   "kv_row_bytes": counts["row_bytes"]},
+                   "kv_row_bytes": counts["row_bytes"],
+                   "qk": "fp8" if fp8_qk else "bf16"},
         "us_per_call": round(ms_step * 1e3, 2),
         "gathered_kv_GBps_call": round(counts["rows"] * counts["row_bytes"] / (ms_step * 1e-3)
                                        / 1e9, 1),
@@ -279,13 +297,13 @@ def main():
         "roofline": roof,
         "peaks": {"hbm_GBps": HBM_PEAK_GBPS, "bf16_mfma_TFLOPs": BF16_PEAK_TFLOPS},
     }
-    prof = profiled_counters(args.workload)
+    prof = profiled_counters(prof_key)
     if prof is not None:
         res["profiled_counters"] = prof
     if args.workload in REFERENCE_PUBLISHED:
         res["reference_published"] = REFERENCE_PUBLISHED[args.workload]
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(sets[0], counts)
+        res["cpu_baseline"] = cpu_baseline(sets[0], counts, fp8_qk=fp8_qk)
     print(json.dumps(res), flush=True)
     if args.calibrate_copy > 0:
         n = args.calibrate_copy << 20

@@ -1133,6 +1133,19 @@ __device__ __host__ inline int ring_row_base(int r) {
   return (16 * a + 4 * b + ((c + (b >> 1)) & 3)) * MAIN_ROW_BYTES + 16 * (2 * (b & 1) + a);
 }
 __device__ __host__ inline int ring_rope_slot(int r, int c) { return 8 * r + (c ^ ((r >> 1) & 7)); }
+// fp8 Q·Kᵀ stage: chunk swizzle of row r (row bits 1, 0, 2, 3 to chunk bits 0, 1, 2,
+// 3). A K-operand read (ds_read_b128) has lane l at row 16 rh + l % 16, chunk
+// 8 blk + 2 (l / 16) + h. A b128 read is served 16 lanes per cycle, the lanes of
+// one parity in one 32-lane half (lane bits 0 and 5 fixed): fitted to
+// SQ_LDS_BANK_CONFLICT over single-pattern probe kernels on MI355X (it is the
+// only such grouping under which ring_row_base reads are conflict-free and the
+// dims-split kernel's rotated layout and two earlier fp8 layouts are 2-way
+// conflicted, as measured). Such a cycle holds 8 rows of one parity x 2 chunk
+// pairs, which the swizzle spreads over the 16 bank groups.
+__device__ __host__ inline int k8_swz(int r) {
+  return ((r >> 1) & 1) | ((r & 1) << 1) | (((r >> 2) & 1) << 2) | (((r >> 3) & 1) << 3);
+}
+__device__ __host__ inline int k8_chunk(int r, int c) { return (c & 16) | ((c ^ k8_swz(r)) & 15); }
 
 template <int DQK, int DV, int NHG, typename T, int KVF, bool QK8 = false>
 __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
@@ -1154,11 +1167,12 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   constexpr int STAGE_BYTES = MAIN_BYTES + (ROPE ? ROPE_BYTES : 0);
   constexpr int PB_HG = 32 * 64;         // Pᵀ of one head group: 32 heads x 32 rows x 2 B
   // fp8 Q·Kᵀ (QK8): two stages of the tile's raw e4m3 dims 0..511 (row r at
-  // r * K8_ROW: the 528-byte stride puts the 16 rows of a K-operand read in 16
-  // distinct bank groups) followed by the block scales as [block][row] floats
-  constexpr int K8_ROW = 528;
+  // r * 512, its 16-byte chunk c at chunk (c & 16) | ((c ^ k8_swz(r)) & 15), see
+  // k8_swz) followed by the block scales as [block][row] floats
+  constexpr int K8_ROW = 512;
   constexpr int K8_SCALES = TILE * K8_ROW;
-  constexpr int K8_STAGE = K8_SCALES + 4 * TILE * 4;
+  constexpr int K8_SSTRIDE = 36;  // floats per block of scales (the 4 writers of a row hit 4 banks)
+  constexpr int K8_STAGE = K8_SCALES + 4 * K8_SSTRIDE * 4;
   constexpr int K8_BASE = NSTG * STAGE_BYTES + (ROPE ? 0 : NHG * PB_HG);
   constexpr int ROWS_PER_WAVE = TILE / NW;             // main-part DMA instructions per wave
   constexpr int NROPE = ROPE ? TILE / 8 : 0;           // rope DMA instructions per tile (4)
@@ -1342,8 +1356,11 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       const int ntile = (clen + TILE - 1) / TILE;
       // query fragment of the item (first chunk): compiler-visible loads issued
       // before the resolution's loads, so they land during its memory round
-      // trips; the compiler's wait for the table words below covers them
-      if (c0 == p_lo) {
+      // trips; the compiler's wait for the table words below covers them.
+      // (fp8 Q·Kᵀ: loaded and quantized again for every chunk, so nothing of the
+      // query is carried across the chunk loop but its e4m3 form within a chunk:
+      // a carried bf16 copy next to the e4m3 one spilled the resolution's registers)
+      if (QK8 || c0 == p_lo) {
         const int head_q = hb * MB + hq;
         const bool hok = head_q < a.num_heads && tok_ok;
         const short* qrow = (const short*)a.q + ((size_t)(tok_ok ? tok : 0) * a.num_heads +
@@ -1450,7 +1467,7 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
       if (c0 == p_lo) m_run = seed_m();
       if constexpr (QK8) {
-        if (c0 == p_lo) quantize_q(qf, q8, sq);
+        quantize_q(qf, q8, sq);
       }
       if (stop_pending) {
         __syncthreads();  // every thread's atomicMin is in
@@ -1585,8 +1602,8 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
 #pragma unroll
           for (int j = 0; j < ROWS_PER_WAVE; ++j) {
             const int r = w + NW * j;
-            *(uint2*)(kb8 + r * K8_ROW + 8 * lane) = f.v[j];
-            if ((lane & 15) == 0) *(float*)(kb8 + K8_SCALES + 4 * ((lane >> 4) * TILE + r)) = f.s[j];
+            *(uint2*)(kb8 + r * K8_ROW + 16 * k8_chunk(r, lane >> 1) + 8 * (lane & 1)) = f.v[j];
+            if ((lane & 15) == 0) *(float*)(kb8 + K8_SCALES + 4 * ((lane >> 4) * K8_SSTRIDE + r)) = f.s[j];
           }
         }
         // the lane's RPL rope bytes: whole 16-byte chunks (RPL 16; consecutive chunks
@@ -1630,14 +1647,14 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
         return (lds_p)(kv_base + (uint32_t)(K8_BASE + (tile & 1) * K8_STAGE));
       };
       auto k8op = [&](lds_p kb8, int blk) -> i32x8 {
-        const lds_p p = kb8 + k_row * K8_ROW + 128 * blk + 32 * g4;
-        const i32x4 lo = *(const i32x4 SAS_LDS*)p;
-        const i32x4 hi = *(const i32x4 SAS_LDS*)(p + 16);
+        const lds_p p = kb8 + k_row * K8_ROW;
+        const i32x4 lo = *(const i32x4 SAS_LDS*)(p + 16 * k8_chunk(k_row, 8 * blk + 2 * g4));
+        const i32x4 hi = *(const i32x4 SAS_LDS*)(p + 16 * k8_chunk(k_row, 8 * blk + 2 * g4 + 1));
         return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       };
       // block blk's scales of the wave's output rows 16 rh + 4 g4 + i (element i)
       auto k8scale = [&](lds_p kb8, int blk) -> f32x4 {
-        return *(const f32x4 SAS_LDS*)(kb8 + K8_SCALES + 4 * (blk * TILE + 16 * rh + 4 * g4));
+        return *(const f32x4 SAS_LDS*)(kb8 + K8_SCALES + 4 * (blk * K8_SSTRIDE + 16 * rh + 4 * g4));
       };
       auto mma8 = [&](i32x8 x, i32x8 y) -> f32x4 {
         // e4m3 x e4m3 (format selectors 0), no block scaling: v_mfma_f32_16x16x128_f8f6f4
