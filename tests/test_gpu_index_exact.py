@@ -16,7 +16,8 @@ top-k lists wider than one resolution chunk (1024 positions) fit in pools of
 at most 256 rows. Covered: windows -1 / 0 / 5 / 7 / 63 / 127 / 1023, ragged TND rows,
 dense compressed thresholds at ratios 4 and 16, top-k with -1 in the middle,
 ids >= thr, duplicates, all -1 rows, items of more than 1024 positions, split
-items (few workgroups), H = 16 / 64 / 128, d_qk 512 / 576, bf16 and fp8 rows.
+items (few workgroups), H = 16 / 64 / 128, d_qk 512 / 576, bf16 and fp8 rows, and
+the fp8 Q·Kᵀ form (q = 0 quantizes to all-zero codes, so every score is still 0).
 """
 
 import math
@@ -221,9 +222,24 @@ def test_topk_rows_exact(win, cores):
 
 
 @requires_gpu
-def test_topk_rows_exact_fp8_rows():
-    _say("SCFA top-k, fp8 rows")
+@pytest.mark.parametrize("fp8_qk", [False, True])
+def test_topk_rows_exact_fp8_rows(fp8_qk):
+    # fp8 rows through the pipelined kernel, Q·Kᵀ in bf16 or on fp8 MFMA (q = 0
+    # quantizes to all-zero codes, so every score is still 0)
+    _say(f"SCFA top-k, fp8 rows, fp8_qk={fp8_qk}")
     kw, idx, t1, t2 = _case(scenario=3, layout="BSND", qlens=[1, 1, 1], kvlens=[700, 2100, 90],
                             heads=64, d=576, win=3, ratio=4, k=300, bs1=16, bs2=16, seed=5,
                             edit=_edits, fp8=True)
-    _check(kw, idx, t1, t2, 3, 4, 16, 16)
+    _check(kw, idx, t1, t2, 3, 4, 16, 16, fp8_qk=fp8_qk)
+
+
+@requires_gpu
+@pytest.mark.parametrize("cores", [256, 7])
+def test_topk_rows_exact_fp8_qk_two_chunks(cores):
+    # the fp8 Q·Kᵀ form requantizes the query for each resolution chunk: items of
+    # more than 1024 positions (two chunks), split over 7 workgroups or not
+    _say(f"SCFA top-k 1030, fp8 rows, fp8 Q·Kᵀ, cores {cores}")
+    kw, idx, t1, t2 = _case(scenario=3, layout="TND", qlens=[2, 1, 1], kvlens=[3000, 2500, 1100],
+                            heads=128, d=576, win=63, ratio=1, k=1030, bs1=16, bs2=16, seed=6,
+                            edit=_edits, fp8=True)
+    _check(kw, idx, t1, t2, 3, 1, 16, 16, core_num=cores, fp8_qk=True)
