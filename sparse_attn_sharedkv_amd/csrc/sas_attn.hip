@@ -1177,7 +1177,9 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   constexpr int ROWS_PER_WAVE = TILE / NW;             // main-part DMA instructions per wave
   constexpr int NROPE = ROPE ? TILE / 8 : 0;           // rope DMA instructions per tile (4)
   constexpr int DMA_MAX = ROWS_PER_WAVE + (ROPE ? 1 : 0);  // per wave and tile (waves w < NROPE)
-  constexpr int RCH = 1024;              // positions resolved into LDS at a time
+  // positions resolved into LDS at a time (the fp8 Q·Kᵀ form with 64-head items:
+  // 2048, so 2048-row items are one chunk and the query is quantized once)
+  constexpr int RCH = (QK8 && NHG == 2) ? 2048 : 1024;
   static_assert(DQK == 512 || DQK == 576, "head_dim");
   static_assert(DV == 512, "head_dim_v");
   static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
