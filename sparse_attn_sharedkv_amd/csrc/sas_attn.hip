@@ -1161,9 +1161,9 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   constexpr int DVQ = DV / 4;            // dv per wave (a quarter)
   constexpr int DVB = DVQ / 32;          // 32-wide dv blocks per wave (4)
   // LDS ring depth: the DMA path keeps tile it + 3 in flight; fp8 rows fill tile
-  // it + 2 from registers, which three stages hold (the fp8 Q·Kᵀ form needs the
-  // space of the fourth for its e4m3 K stages)
-  constexpr int NSTG = QK8 ? 3 : 4;
+  // it + 2 from registers, which three stages hold (the space of the fourth goes
+  // to a longer row-id buffer and, in the fp8 Q·Kᵀ form, the e4m3 K stages)
+  constexpr int NSTG = FP8 ? 3 : 4;
   constexpr int STAGE_BYTES = MAIN_BYTES + (ROPE ? ROPE_BYTES : 0);
   constexpr int PB_HG = 32 * 64;         // Pᵀ of one head group: 32 heads x 32 rows x 2 B
   // fp8 Q·Kᵀ (QK8): two stages of the tile's raw e4m3 dims 0..511 (row r at
@@ -1177,9 +1177,10 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   constexpr int ROWS_PER_WAVE = TILE / NW;             // main-part DMA instructions per wave
   constexpr int NROPE = ROPE ? TILE / 8 : 0;           // rope DMA instructions per tile (4)
   constexpr int DMA_MAX = ROWS_PER_WAVE + (ROPE ? 1 : 0);  // per wave and tile (waves w < NROPE)
-  // positions resolved into LDS at a time (the fp8 Q·Kᵀ form with 64-head items:
-  // 2048, so 2048-row items are one chunk and the query is quantized once)
-  constexpr int RCH = (QK8 && NHG == 2) ? 2048 : 1024;
+  // positions resolved into LDS at a time (fp8 rows with 64-head items: 2048, so a
+  // 2048-row item is one chunk: one resolution, one pipeline start and, in the
+  // fp8 Q·Kᵀ form, one quantization of the query)
+  constexpr int RCH = (FP8 && NHG == 2) ? 2048 : 1024;
   static_assert(DQK == 512 || DQK == 576, "head_dim");
   static_assert(DV == 512, "head_dim_v");
   static_assert((STAGE_BYTES % 1024) == 0, "stage alignment");
