@@ -115,14 +115,33 @@ def test_reference_fast_prefill(name):
 
 
 @requires_gpu
+@pytest.mark.parametrize("name", ["swa_prefill_fast", "cfa_prefill_fast", "scfa_prefill_fast"])
+def test_flash_mla_fast_scenarios(name):
+    # the flash-MLA twin's self-test (sparse_flash_mla_api.py:256-272) runs its
+    # FAST_SCENARIOS (sparse_flash_mla_golden.py:391-461: S1 = 1024, H = 64, d 512,
+    # block_num1 10, block_num2 1 / 2 / 3) through sparse_flash_mla; the shrunk
+    # reference cases have exactly those parameters
+    _say(f"flash-MLA fast scenario {name}")
+    cfg = gen.FAST_CASES[name]
+    assert (cfg["S1"], cfg["N1"], cfg["D"], cfg["block_num1"]) == (1024, 64, 512, 10)
+    assert cfg["block_num2"] == {1: 1, 2: 2, 3: 3}[cfg["scenario"]]
+    kw = gen.build_case(cfg, torch.bfloat16)
+    out, lse = _run(kw, fn=sparse_flash_mla)
+    _check_reference_regime(out, lse, kw, torch.bfloat16)
+
+
+@requires_gpu
+@pytest.mark.parametrize("entry", ["sparse_attn_sharedkv", "sparse_flash_mla"])
 @pytest.mark.parametrize("name", ["swa_prefill", "cfa_prefill", "scfa_prefill"])
-def test_reference_prefill_full_size_sampled_tokens(name):
-    # the reference's own 8K prefill cases (test_sparse_attn_sharedkv.py:105-220)
-    # at full size; the oracle checks query rows at the start, around the window
-    # and compressed-threshold edges, in the middle and at the end
-    _say(f"full-size reference prefill {name} (sampled)")
+def test_reference_prefill_full_size_sampled_tokens(name, entry):
+    # the reference's own 8K prefill cases (test_sparse_attn_sharedkv.py:105-220,
+    # and the same parameters as the flash-MLA twin's FULL_SCENARIOS,
+    # sparse_flash_mla_test_full.py:5-29) at full size through either entry
+    # point; the oracle checks query rows at the start, around the window and
+    # compressed-threshold edges, in the middle and at the end
+    _say(f"full-size reference prefill {name} via {entry} (sampled)")
     kw = gen.build_case(gen.REFERENCE_CASES[name], torch.bfloat16)
-    out, lse = _run(kw)
+    out, lse = _run(kw, fn=sparse_flash_mla if entry == "sparse_flash_mla" else None)
     total = kw["q"].shape[0]
     toks = sorted({0, 1, 3, 126, 127, 128, 129, 511, 512, 2047, 2048, 2049, 4095, 6143,
                    total - 2, total - 1})
