@@ -4,7 +4,7 @@ Cases follow the reference's suites: decode at kv = 8193 for SWA / CFA / SCFA
 in bf16 and fp16 (test_sparse_attn_sharedkv.py:81-235, :586-605), the shrunk
 prefill cases including the ragged two-sequence ones
 (test_sparse_attn_sharedkv_fast.py:147-179), the full 8K prefill cases on
-sampled query rows, the return-type contract
+every query row through both entry points, the return-type contract
 (:608-715) and the metadata-then-kernel flow (:484-583). Beyond them: the
 benchmark shapes (H = 16 / 64 / 128, d_qk = 576 with d_v = 512, pure top-k,
 MTP), split-KV invariance, index edge cases, and the full-size DeepSeek-V3.2
@@ -23,6 +23,7 @@ Acceptance:
   accurate as golden.
 """
 
+import functools
 import math
 import sys
 
@@ -130,29 +131,38 @@ def test_flash_mla_fast_scenarios(name):
     _check_reference_regime(out, lse, kw, torch.bfloat16)
 
 
-@requires_gpu
-@pytest.mark.parametrize("entry", ["sparse_attn_sharedkv", "sparse_flash_mla"])
-@pytest.mark.parametrize("name", ["swa_prefill", "cfa_prefill", "scfa_prefill"])
-def test_reference_prefill_full_size_sampled_tokens(name, entry):
-    # the reference's own 8K prefill cases (test_sparse_attn_sharedkv.py:105-220,
-    # and the same parameters as the flash-MLA twin's FULL_SCENARIOS,
-    # sparse_flash_mla_test_full.py:5-29) at full size through either entry
-    # point; the oracle checks query rows at the start, around the window and
-    # compressed-threshold edges, in the middle and at the end
-    _say(f"full-size reference prefill {name} via {entry} (sampled)")
+@functools.lru_cache(maxsize=1)
+def _full_prefill_case(name):
+    """Inputs, the oracle over every query row, and the float64 closed form on
+    sampled rows (start, around the window and compressed-threshold edges,
+    middle, end) for one of the reference's 8K prefill cases; kept for the
+    next test, which runs the same case through the other entry point."""
     kw = gen.build_case(gen.REFERENCE_CASES[name], torch.bfloat16)
-    out, lse = _run(kw, fn=sparse_flash_mla if entry == "sparse_flash_mla" else None)
+    okw = {k: v for k, v in kw.items() if k not in ("topk_cmp",)}
+    ref, ref_lse = sparse_attn_oracle(**okw)
     total = kw["q"].shape[0]
     toks = sorted({0, 1, 3, 126, 127, 128, 129, 511, 512, 2047, 2048, 2049, 4095, 6143,
                    total - 2, total - 1})
-    okw = {k: v for k, v in _cpu(kw).items() if k not in ("topk_cmp",)}
-    ref, ref_lse = sparse_attn_oracle(**okw, tokens=toks)
     ex, _ = sparse_attn_exact(**okw, tokens=toks)
-    o, l = out.cpu()[toks], lse.cpu()[toks]
+    return kw, ref, ref_lse, toks, ex[toks]
+
+
+@requires_gpu
+@pytest.mark.parametrize("entry", ["sparse_attn_sharedkv", "sparse_flash_mla"])
+@pytest.mark.parametrize("name", ["swa_prefill", "cfa_prefill", "scfa_prefill"])
+def test_reference_prefill_full_size(name, entry):
+    # the reference's own 8K prefill cases (test_sparse_attn_sharedkv.py:105-220,
+    # the same parameters as the flash-MLA twin's FULL_SCENARIOS,
+    # sparse_flash_mla_test_full.py:5-40) at full size through either entry
+    # point, every query row against the oracle by the reference's rule
+    _say(f"full-size reference prefill {name} via {entry}")
+    kw, ref, ref_lse, toks, ex = _full_prefill_case(name)
+    out, lse = _run(kw, fn=sparse_flash_mla if entry == "sparse_flash_mla" else None)
+    out, lse = out.cpu(), lse.cpu()
     assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
-    check_result(o, ref[toks])
-    check_lse(l, ref_lse[toks], torch.bfloat16)
-    check_vs_exact(o, ref[toks], ex[toks])
+    check_result(out, ref)
+    check_lse(lse, ref_lse, torch.bfloat16)
+    check_vs_exact(out[toks], ref[toks], ex)
 
 
 @requires_gpu
