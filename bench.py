@@ -73,10 +73,25 @@ def parse():
     return ap.parse_args()
 
 
-def measured_traffic(workload):
-    """HBM bytes per attention launch from the committed rocprofv3 PMC summary, or None."""
+def summary_kernel(path):
+    """The kernel a committed rocprofv3 summary measured: its ``# kernel:`` header line, else
+    the ``sas::...`` name in its first line."""
+    with open(path, encoding="utf-8") as f:
+        lines = f.readlines()
+    for line in lines:
+        if line.startswith("# kernel:"):
+            return line.split(":", 1)[1].strip()
+    for tok in (lines[0].split() if lines else []):
+        if tok.startswith("sas::"):
+            return tok.rstrip(",")
+    return None
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary of ``kernel``,
+    or None (no summary, or one of another kernel)."""
     path = os.path.join(ROOT, "profiles", f"attn_kernel_{workload}_pmc.txt")
-    if not os.path.exists(path):
+    if not os.path.exists(path) or summary_kernel(path) != kernel:
         return None
     for line in open(path, encoding="utf-8"):
         if line.startswith("traffic_bytes_per_launch:"):
@@ -84,14 +99,38 @@ def measured_traffic(workload):
     return None
 
 
-def profiled_counters(workload):
+def kernel_source_sha16():
+    """First 16 hex digits of the SHA-256 over the kernel sources (csrc/*.hip, *.h, *.cpp in
+    name order): the fingerprint a counter summary records for the code it measured."""
+    import hashlib
+
+    d = os.path.join(ROOT, "sparse_attn_sharedkv_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".hip", ".h", ".cpp")):
+            h.update(name.encode())
+            h.update(open(os.path.join(d, name), "rb").read())
+    return h.hexdigest()[:16]
+
+
+def profiled_counters(workload, kernel):
     """MFMA / VALU / LDS activity of the attention kernel from the committed rocprofv3 SQ
-    counter summary (``profiles/attn_kernel_<workload>_sq.txt``), or None."""
+    counter summary (``profiles/attn_kernel_<workload>_sq.txt``), or None.
+
+    The summary's header names the kernel it measured (``# kernel: ...``) and the
+    fingerprint of the sources it was built from (``# source_sha16: ...``). A summary of
+    another kernel is not used; one whose fingerprint differs from the current sources
+    is reported with ``"stale": true``."""
     path = os.path.join(ROOT, "profiles", f"attn_kernel_{workload}_sq.txt")
     if not os.path.exists(path):
         return None
     out = {}
+    meta = {"kernel": summary_kernel(path)}
     for line in open(path, encoding="utf-8"):
+        if line.startswith("# source_sha16:") or line.startswith("# measured_commit:"):
+            key, val = line[1:].split(":", 1)
+            meta[key.strip()] = val.strip()
+            continue
         if ":" in line and not line.startswith("#"):
             key, val = line.split(":", 1)
             key = key.strip()
@@ -101,9 +140,12 @@ def profiled_counters(workload):
                     out[key] = float(val.split()[0])
                 except ValueError:
                     pass
-    if not out:
+    if not out or meta.get("kernel") != kernel:
         return None
     out["source"] = os.path.relpath(path, ROOT)
+    out["measured_commit"] = meta.get("measured_commit")
+    out["source_sha16"] = meta.get("source_sha16")
+    out["stale"] = meta.get("source_sha16") != kernel_source_sha16()
     return out
 
 
@@ -232,8 +274,10 @@ def main():
     srt = attn_ms
 
     achieved = nbytes / (attn_avg * 1e-3) / 1e9
-    # native rows run on the one-wave-per-SIMD kernel, fp8 rows on the pipelined one
-    kernel = "sas::attn3_kernel" if sets[0].get("kv_cache_dtype") else "sas::attn2_kernel"
+    # fp8 rows run on the pipelined kernel; native rows on the 128-head kernel when
+    # an item holds 128 heads, else on the one-wave-per-SIMD kernel
+    kernel = ("sas::attn3_kernel" if sets[0].get("kv_cache_dtype")
+              else "sas::wide_kernel" if preps[0].args.m_base == 128 else "sas::attn2_kernel")
     if w.get("prefill"):
         # prefill: consecutive query rows re-read each other's cache rows, which
         # stay on chip; the algorithmic HBM bytes are q, out and lse once plus the
@@ -245,20 +289,20 @@ def main():
             ach = pbytes / (attn_avg * 1e-3) / 1e9
             roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                    "traffic": measured_traffic(prof_key), "algorithmic_bytes": int(pbytes),
+                    "traffic": measured_traffic(prof_key, kernel), "algorithmic_bytes": int(pbytes),
                     "kernel": kernel}
         else:
             ach = flops / (attn_avg * 1e-3) / 1e12
             roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
-                    "traffic": measured_traffic(prof_key), "algorithmic_bytes": int(pbytes),
+                    "traffic": measured_traffic(prof_key, kernel), "algorithmic_bytes": int(pbytes),
                     "kernel": kernel}
         roof["hbm_time_us"] = round(t_hbm * 1e6, 1)
         roof["mfma_time_us"] = round(t_mfma * 1e6, 1)
     else:
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                "traffic": measured_traffic(prof_key), "algorithmic_bytes": int(nbytes),
+                "traffic": measured_traffic(prof_key, kernel), "algorithmic_bytes": int(nbytes),
                 "kernel": kernel}
     res = {
         "metric": METRIC,
@@ -297,7 +341,7 @@ def main():
         "roofline": roof,
         "peaks": {"hbm_GBps": HBM_PEAK_GBPS, "bf16_mfma_TFLOPs": BF16_PEAK_TFLOPS},
     }
-    prof = profiled_counters(prof_key)
+    prof = profiled_counters(prof_key, kernel)
     if prof is not None:
         res["profiled_counters"] = prof
     if args.workload in REFERENCE_PUBLISHED:

@@ -97,14 +97,16 @@ def attend_token_kernel_order(q: torch.Tensor, segments: Sequence[torch.Tensor],
 
 def fp16_partial(o: torch.Tensor) -> torch.Tensor:
     """A split piece's partial rows ``o`` [heads, d_v] (fp32) as the kernels store them:
-    per row, fp16 of ``o * s`` with ``s = 2^(14 - e)`` when the row's largest |value|
-    ``m`` is finite and at least 2^15 (``e = floor(log2 m)``, so ``m * s`` lies in
-    [2^14, 2^15)), else ``s = 1``; returned as fp32 ``fp16(o * s) / s``."""
+    per row, fp16 of ``o * s`` with ``s = 2^(14 - e)``, ``e = max(floor(log2 m), -112)``
+    for the row's largest |value| ``m`` when it is finite and nonzero (so ``m * s``
+    lies in [2^14, 2^15): rows are scaled up or down; the clamp keeps ``s`` and
+    ``1 / s`` normal floats), else ``s = 1``; returned as fp32 ``fp16(o * s) / s``."""
     o = o.to(torch.float32)
     m = o.abs().nan_to_num(nan=0.0).amax(dim=1, keepdim=True)
-    big = (m >= 32768.0) & torch.isfinite(m)
-    e = torch.frexp(torch.where(big, m, torch.ones_like(m)))[1].to(torch.float32) - 1.0
-    s = torch.where(big, torch.exp2(14.0 - e), torch.ones_like(m))
+    ok = (m > 0) & torch.isfinite(m)
+    e = torch.frexp(torch.where(ok, m, torch.ones_like(m)))[1].to(torch.float32) - 1.0
+    e = e.clamp(min=-112.0)
+    s = torch.where(ok, torch.exp2(14.0 - e), torch.ones_like(m))
     return (o * s).to(torch.float16).to(torch.float32) / s
 
 

@@ -77,21 +77,34 @@ class Prepared:
 
 @functools.lru_cache(maxsize=64)
 def _cached_schedule(act_q: tuple, act_kv: tuple, num_heads: int, ori_win_left: int,
-                     scenario: int, cmp_ratio: int, topk: int, core_num: int) -> torch.Tensor:
+                     scenario: int, cmp_ratio: int, topk: int, core_num: int,
+                     fp8: bool) -> torch.Tensor:
     return build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads,
                           ori_win_left=ori_win_left, scenario=scenario, cmp_ratio=cmp_ratio,
-                          cmp_topk=topk, core_num=core_num)
+                          cmp_topk=topk, core_num=core_num, fp8=fp8)
 
 
 # Schedules built by the on-device scheduler for calls without ``metadata``: one
 # library-owned buffer per (device, stream), written only by that scheduler on
 # that stream, so an unchanged schedule is kept instead of rebuilt. Calls on one
 # stream run in order; different streams get different buffers.
+# A call captured into a HIP graph gets a buffer of its own instead (graphs
+# captured on one stream may be replayed on different streams, or beside eager
+# calls on the capture stream, so a shared buffer would race); it is allocated
+# from the capture's pool and kept for the life of the process, because every
+# replay of the graph reads and writes it. Its first replay builds the schedule,
+# later replays keep it while the lengths give the same schedule.
 _DEVICE_SCHEDULES: dict = {}
+_CAPTURED_SCHEDULES: list = []
 _DEVICE_SCHEDULES_LOCK = threading.Lock()
 
 
 def _schedule_buffer(dev: torch.device) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        buf = torch.empty(SAS_META_SIZE, dtype=torch.int32, device=dev)
+        with _DEVICE_SCHEDULES_LOCK:
+            _CAPTURED_SCHEDULES.append(buf)
+        return buf
     st = torch.cuda.current_stream(dev)
     key = (dev.index, st.cuda_stream)
     with _DEVICE_SCHEDULES_LOCK:
@@ -120,7 +133,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             kv_cache_dtype: Optional[str] = None,
             schedule: Optional[str] = None,
             fp8_qk: bool = False,
-            _stream_schedule: bool = False) -> Prepared:
+            _stream_schedule: bool = False,
+            _pipelined: bool = False) -> Prepared:
     """Validate and stage one call (host work of api.py:186-384) without launching.
 
     ``schedule``: ``"host"`` reads the lengths back and schedules on the CPU (the
@@ -130,7 +144,9 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     ``"host"`` otherwise. ``_stream_schedule`` (for callers that launch right after
     preparing, on the same stream): a device-built schedule goes to the library's
     buffer for the current stream and is kept when unchanged; otherwise every
-    prepared call schedules into a buffer of its own.
+    prepared call schedules into a buffer of its own. ``_pipelined`` (tests): native
+    rows run through the kernel fp8 rows use (``SAS_PHASE_PIPELINED``, items of at
+    most 64 heads), for bitwise comparisons with the fp8 path.
     """
     del seqused_q  # API-parity placeholder (api.py:186)
     assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
@@ -202,9 +218,11 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
         n2 = ori_kv.shape[2]
 
     kv_fmt = _kv_format(kv_cache_dtype, ori_kv)
-    fp8 = kv_fmt == _lib.KV_FP8_DS_MLA
-    row_width = _lib.FP8_ROW_BYTES if fp8 else d
-    dv = (512 if fp8 else d) if head_dim_v is None else int(head_dim_v)
+    fp8_rows = kv_fmt == _lib.KV_FP8_DS_MLA
+    # items of at most 64 heads: fp8 rows and the pipelined kernel (m_base_for)
+    item64 = fp8_rows or _pipelined
+    row_width = _lib.FP8_ROW_BYTES if fp8_rows else d
+    dv = (512 if fp8_rows else d) if head_dim_v is None else int(head_dim_v)
     if n2 != 1 or ori_kv.shape[2] != 1 or ori_kv.shape[-1] != row_width:
         raise ValueError(f"only N2=1 shared KV with KV width == q width supported "
                          f"(got N2={n2}, q D={d}, kv {tuple(ori_kv.shape)})")
@@ -213,7 +231,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                          f"{SUPPORTED_HEAD_DIM_V} (got D={d}, head_dim_v={dv})")
     if n1 < 16 or n1 > 128 or n1 % 16 != 0:
         raise ValueError(f"N1 must be a multiple of 16 in [16, 128] (got N1={n1})")
-    if fp8:
+    if fp8_rows:
         if d != 576 or dtype != torch.bfloat16:
             raise ValueError("fp8_ds_mla caches need bf16 queries with D=576")
         for t in (ori_kv, cmp_kv):
@@ -222,7 +240,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                                  f"[blocks, block_size, 1, {_lib.FP8_ROW_BYTES}]")
     elif ori_kv.dtype != dtype or (cmp_kv is not None and cmp_kv.dtype != dtype):
         raise ValueError("KV caches must have q's dtype")
-    if fp8_qk and not fp8:
+    if fp8_qk and not fp8_rows:
         raise ValueError("fp8_qk needs fp8_ds_mla cache rows")
     if ori_win_left < -1:
         raise ValueError("ori_win_left must be >= -1")
@@ -272,7 +290,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                 batch=nb, act_q=act_q_d, act_kv=seqused, num_heads=int(n1),
                 ori_win_left=int(ori_win_left), scenario=scenario, cmp_ratio=cmp_ratio_eff,
                 cmp_topk=int(k), core_num=int(core_num),
-                out=_schedule_buffer(dev) if _stream_schedule else None)
+                out=_schedule_buffer(dev) if _stream_schedule else None, fp8=item64)
         else:
             metadata_dev = metadata.to(device=dev, dtype=i32).reshape(SAS_META_SIZE).contiguous()
         # capacities; the kernels read the schedule's own summary on the GPU. A
@@ -282,18 +300,19 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
         # for the most partial pieces such a schedule can have (two per core).
         cap = int(core_num) if metadata is None else AIC_CORE_NUM
         cfg = dict(num_fa=cap, num_fd=_lib.SCHED_DEVICE, num_partial_slots=2 * cap,
-                   s2_base=DEFAULT_S2_BASE, m_base=m_base_for(n1))
+                   s2_base=DEFAULT_S2_BASE, m_base=m_base_for(n1, item64))
     elif metadata is None:
         kv_host = tuple(int(x) for x in seqused_kv.to(torch.int32).cpu().tolist())
         md = _cached_schedule(tuple(act_q), kv_host, int(n1), int(ori_win_left), scenario,
-                              cmp_ratio_eff, int(k), int(core_num))
+                              cmp_ratio_eff, int(k), int(core_num), item64)
         cfg = config_row(md)
         metadata_dev = md.to(dev, non_blocking=True)
     else:
         metadata_dev = metadata.to(dev).to(torch.int32).reshape(SAS_META_SIZE).contiguous()
         cfg = config_row(metadata)  # host read of the schedule summary row
-        assert cfg["num_heads"] == n1 and cfg["m_base"] == m_base_for(n1), (
-            "metadata was built for a different head count")
+        assert cfg["num_heads"] == n1 and cfg["m_base"] == m_base_for(n1, item64), (
+            "metadata was built for a different head count or cache row format "
+            "(fp8 cache rows: sparse_attn_sharedkv_metadata(..., kv_cache_dtype='fp8_ds_mla'))")
 
     # ---- device tensors ----
     q_flat = q.reshape(total, n1, d).contiguous()
@@ -344,7 +363,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             sinks_d, metadata_dev, out, lse, ws]
     return Prepared(args=a, keep=keep, out=out, lse=lse, layout_q=layout_q,
                     bsnd_shape=None if layout_q == "TND" else (nb, total // max(nb, 1), n1, dv),
-                    device=dev, phase_bits=_lib.SAS_PHASE_FP8_QK if fp8_qk else 0)
+                    device=dev, phase_bits=(_lib.SAS_PHASE_FP8_QK if fp8_qk else 0) |
+                    (_lib.SAS_PHASE_PIPELINED if _pipelined else 0))
 
 
 def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: int = 0) -> None:

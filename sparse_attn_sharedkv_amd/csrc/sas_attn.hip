@@ -237,20 +237,25 @@ __device__ void nan_fill(const SasAttnArgs& a, int tid, int nthreads) {
 }
 
 // Split-KV partials: per (slot, head) the row acc / l as fp16, times a power-of-two
-// scale that keeps the row's largest |value| below 2^15 (1 for every row below
-// that), then fp32 lse [slot][head] and fp32 inverse scales [slot][head].
+// scale that puts the row's largest |value| into [2^14, 2^15) (scaled up or
+// down), then fp32 lse [slot][head] and fp32 inverse scales [slot][head].
 // fp16's 11-bit significand keeps the merged result as close to golden as fp32
-// partials do on the reference's input distribution, at half the bytes.
+// partials do on the reference's input distribution, at half the bytes, and the
+// two-sided normalisation keeps that true for rows of any magnitude: small rows
+// are not left to fp16's subnormal range.
 struct PartialScale {
   float scale, inv;
 };
 __device__ inline PartialScale partial_scale(float row_max) {
-  if (row_max >= 32768.0f && row_max < INFINITY) {
-    const int e = (int)((__float_as_uint(row_max) >> 23) & 0xFF) - 127;  // 15 .. 127
+  if (row_max > 0.0f && row_max < INFINITY) {
+    // row_max = 1.f * 2^e; e clamped to [-112, 127] so that scale = 2^(14 - e) and
+    // inv = 2^(e - 14) are both normal floats (rows below 2^-112 are scaled by 2^126)
+    int e = (int)((__float_as_uint(row_max) >> 23) & 0xFF) - 127;
+    e = e < -112 ? -112 : e;
     return {__uint_as_float((uint32_t)(127 + 14 - e) << 23),
             __uint_as_float((uint32_t)(127 + e - 14) << 23)};
   }
-  return {1.0f, 1.0f};
+  return {1.0f, 1.0f};  // an all-zero (or non-finite) row
 }
 __device__ inline float* partial_lse(const SasAttnArgs& a, int mb, int dv) {
   return (float*)((char*)a.workspace + (size_t)a.num_partial_slots * mb * dv * 2);
@@ -2012,6 +2017,12 @@ __global__ __launch_bounds__(256 * NHG) void attn3_kernel(const SasAttnArgs a) {
   }
 }
 
+}  // namespace sas
+
+#include "sas_attn_wide.h"
+
+namespace sas {
+
 // ---------------------------------------------------------------------------
 // Split-KV merge: lse = log(e^sink + Σ e^lse_i), out = Σ e^(lse_i - lse) o_i
 // ---------------------------------------------------------------------------
@@ -2207,6 +2218,9 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
       else
         hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
                            dim3(256 * NHG), 0, st, a);
+    } else if constexpr (NHG == 4) {
+      // 128-head items: one workgroup of 8 waves holds every head of the token
+      hipLaunchKernelGGL((wide_kernel<DQK, 512, T>), dim3(8 * per_xcd), dim3(512), 0, st, a);
     } else {
       if (a.phases & SAS_PHASE_PIPELINED)
         hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
@@ -2232,14 +2246,18 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
-// Items carry m_base = 32 or 64 heads (one or two 32-head groups of four
-// dims-quarter waves): 4 or 8 waves, one or two per SIMD.
+// Items carry m_base = 32 or 64 heads (one or two 32-head groups: attn2_kernel,
+// 2 or 4 waves, one per SIMD) or 128 heads (wide_kernel, 8 waves, two per SIMD).
 template <typename T>
 static hipError_t dispatch_heads(const SasAttnArgs& a, hipStream_t st) {
   constexpr int NAT = SAS_KV_NATIVE;
   if (a.head_dim == 576)
-    return a.m_base == 32 ? launch_attn<576, 1, T, NAT>(a, st) : launch_attn<576, 2, T, NAT>(a, st);
-  return a.m_base == 32 ? launch_attn<512, 1, T, NAT>(a, st) : launch_attn<512, 2, T, NAT>(a, st);
+    return a.m_base == 32   ? launch_attn<576, 1, T, NAT>(a, st)
+           : a.m_base == 64 ? launch_attn<576, 2, T, NAT>(a, st)
+                            : launch_attn<576, 4, T, NAT>(a, st);
+  return a.m_base == 32   ? launch_attn<512, 1, T, NAT>(a, st)
+         : a.m_base == 64 ? launch_attn<512, 2, T, NAT>(a, st)
+                          : launch_attn<512, 4, T, NAT>(a, st);
 }
 
 // fp8 rows: head_dim 576, bf16 queries and outputs
@@ -2274,9 +2292,14 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     set_error("sas_attention_launch: num_heads must be a multiple of 16 in [16, 128]");
     return SAS_E_UNSUPPORTED;
   }
-  if ((a->m_base != 32 && a->m_base != 64) || (a->num_heads <= 32 && a->m_base != 32) ||
-      (a->num_heads > 32 && a->m_base != 64)) {
-    set_error("sas_attention_launch: m_base must be 32 for <= 32 heads, else 64");
+  // heads per item: 32 up to 32 heads, 64 up to 64 heads, above that 128 for native
+  // rows (one item holds the token's every head) and 64 for fp8 rows and for native
+  // rows run through the pipelined kernel (SAS_PHASE_PIPELINED)
+  const bool item64 = a->kv_format == SAS_KV_FP8_DS_MLA || (a->phases & SAS_PHASE_PIPELINED);
+  const int want_mb = a->num_heads <= 32 ? 32 : (a->num_heads <= 64 || item64) ? 64 : 128;
+  if (a->m_base != want_mb) {
+    set_error("sas_attention_launch: m_base must be 32 for <= 32 heads, 64 for <= 64 heads "
+              "(or fp8 rows, or SAS_PHASE_PIPELINED), else 128");
     return SAS_E_INVALID;
   }
   if (a->scenario < 1 || a->scenario > 3 || (a->scenario >= 2 && (!a->cmp_kv ||

@@ -44,9 +44,24 @@ DEFAULT_MIN_SPLIT_BLOCKS = 2  # never split an item into pieces shorter than 128
 DEFAULT_FD_HEAD_CHUNK = 64    # heads per merge task (a whole 64-head item)
 
 
-def m_base_for(num_heads: int) -> int:
-    """Heads per schedulable item (the reference's mBaseSize): 32 or 64."""
-    return 32 if num_heads <= 32 else 64
+def m_base_for(num_heads: int, fp8: bool = False) -> int:
+    """Heads per schedulable item (the reference's mBaseSize, metadata.py:388).
+
+    32 up to 32 heads and 64 up to 64 heads, as the reference; above 64 heads an
+    item holds all of a token's heads (128) for native bf16 / fp16 rows, whose
+    kernel serves every head of the token from one gathered tile, and stays 64
+    for fp8 cache rows (``fp8=True``)."""
+    if num_heads <= 32:
+        return 32
+    return 64 if (num_heads <= 64 or fp8) else 128
+
+
+def _is_fp8(kv_cache_dtype) -> bool:
+    if kv_cache_dtype in (None, "auto"):
+        return False
+    if kv_cache_dtype == "fp8_ds_mla":
+        return True
+    raise ValueError(f"unsupported kv_cache_dtype {kv_cache_dtype!r} (None, 'auto' or 'fp8_ds_mla')")
 
 
 def _as_list(t) -> List[int]:
@@ -90,8 +105,9 @@ def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: in
                    ori_win_left: int, scenario: int, cmp_ratio: int, cmp_topk: int,
                    core_num: int = DEFAULT_CORE_NUM, s2_base: int = DEFAULT_S2_BASE,
                    min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
-                   fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK) -> torch.Tensor:
-    """Run the C++ scheduler; returns an int32 CPU tensor of ``SAS_META_SIZE`` words."""
+                   fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK, fp8: bool = False) -> torch.Tensor:
+    """Run the C++ scheduler; returns an int32 CPU tensor of ``SAS_META_SIZE`` words.
+    ``fp8``: the schedule is for fp8 cache rows (64-head items, ``m_base_for``)."""
     lib = _lib.load()
     b = len(act_q)
     out = torch.zeros(SAS_META_SIZE, dtype=torch.int32)
@@ -99,7 +115,7 @@ def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: in
     ak = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_kv])
     i32p = ctypes.POINTER(ctypes.c_int32)
     rc = lib.sas_metadata_build(ctypes.cast(out.data_ptr(), i32p), b, aq, ak, int(num_heads),
-                                m_base_for(int(num_heads)), int(ori_win_left), int(scenario),
+                                m_base_for(int(num_heads), fp8), int(ori_win_left), int(scenario),
                                 int(cmp_ratio), int(cmp_topk), int(core_num), int(s2_base),
                                 int(min_split_blocks), int(fd_head_chunk))
     if rc < 0:
@@ -152,7 +168,7 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
                           min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
                           fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK,
                           stream: Optional[torch.cuda.Stream] = None,
-                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          out: Optional[torch.Tensor] = None, fp8: bool = False) -> torch.Tensor:
     """Run the on-device scheduler (``sas_metadata_build_device``) on the current stream.
 
     ``act_q`` / ``act_kv``: int32 ``[batch]`` tensors on the GPU (``act_q`` None: every
@@ -186,7 +202,7 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
     rc = lib.sas_metadata_build_device(
         ctypes.c_void_p(out.data_ptr()), int(batch),
         ctypes.c_void_p(act_q.data_ptr() if act_q is not None else 0), int(uniform_q),
-        ctypes.c_void_p(act_kv.data_ptr()), int(num_heads), m_base_for(int(num_heads)),
+        ctypes.c_void_p(act_kv.data_ptr()), int(num_heads), m_base_for(int(num_heads), fp8),
         int(ori_win_left), int(scenario), int(cmp_ratio), int(cmp_topk), int(core_num),
         int(s2_base), int(min_split_blocks), int(fd_head_chunk), int(reuse),
         ctypes.c_void_p(st.cuda_stream))
@@ -231,6 +247,7 @@ def sparse_attn_sharedkv_metadata(
     aic_core_num: int = DEFAULT_CORE_NUM,
     aiv_core_num: int = 2 * DEFAULT_CORE_NUM,
     device: Optional[str] = None,
+    kv_cache_dtype: Optional[str] = None,
 ) -> torch.Tensor:
     """Schedule for one ``sparse_attn_sharedkv`` call: int32 ``[SAS_META_SIZE]``.
 
@@ -243,7 +260,9 @@ def sparse_attn_sharedkv_metadata(
     parity; merge tasks are bounded by ``AIV_CORE_NUM``. With ``device`` a GPU the
     schedule is built there by the on-device scheduler from the lengths moved to
     (or already on) that GPU, without reading them back; the words are the ones
-    the host scheduler produces.
+    the host scheduler produces. ``kv_cache_dtype`` (no reference counterpart):
+    ``"fp8_ds_mla"`` builds the schedule for calls on fp8 cache rows, whose items
+    hold at most 64 heads (``m_base_for``).
     """
     del cu_seqlens_cmp_kv, head_dim, ori_topk, aiv_core_num
     if num_heads_kv != 1:
@@ -261,6 +280,7 @@ def sparse_attn_sharedkv_metadata(
     else:
         scenario = 1
     core_num = min(int(aic_core_num), AIC_CORE_NUM)
+    fp8 = _is_fp8(kv_cache_dtype)
     if device is not None and torch.device(device).type == "cuda":
         # scheduled on that GPU from device-resident lengths: nothing is read back
         batch, act_q, uniform_q, act_kv = device_lengths(
@@ -271,7 +291,7 @@ def sparse_attn_sharedkv_metadata(
                                      act_kv=act_kv, num_heads=num_heads_q,
                                      ori_win_left=ori_win_left, scenario=scenario,
                                      cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
-                                     core_num=core_num)
+                                     core_num=core_num, fp8=fp8)
     act_q, act_kv = resolve_lengths(layout_q=layout_q, layout_kv=layout_kv,
                                     cu_seqlens_q=cu_seqlens_q,
                                     cu_seqlens_ori_kv=cu_seqlens_ori_kv, seqused_q=seqused_q,
@@ -280,5 +300,5 @@ def sparse_attn_sharedkv_metadata(
     md = build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads_q,
                         ori_win_left=ori_win_left, scenario=scenario,
                         cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
-                        core_num=core_num)
+                        core_num=core_num, fp8=fp8)
     return md.to(device) if device is not None else md

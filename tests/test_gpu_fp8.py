@@ -165,8 +165,8 @@ def test_fp8_attention_matches_oracle(heads, k, lens, sinks):
 def _run_pipelined(kw, **extra):
     """Native rows through the kernel fp8 rows use (SAS_PHASE_PIPELINED)."""
     kw = {k: v for k, v in _dev(kw).items() if k != "topk_cmp"}
-    prep = api.prepare(**kw, **extra)
-    api.launch(prep, phases=_lib.SAS_PHASE_PIPELINED)
+    prep = api.prepare(**kw, **extra, _pipelined=True)  # 64-head items, SAS_PHASE_PIPELINED
+    api.launch(prep)
     torch.cuda.synchronize()
     return prep.out.clone(), prep.lse.clone()
 

@@ -95,7 +95,8 @@ def test_fp8_random_configuration(i, qk):
         max_seqlen_kv=max(cfg["seqused_kv"]),
         cmp_topk=cfg["K"] if cfg["scenario"] == 3 else 0, cmp_ratio=cfg["cmp_ratio"],
         ori_win_left=cfg["ori_win_left"], layout_q=cfg["layout_q"],
-        has_cmp_kv=cfg["scenario"] >= 2, aic_core_num=cfg["cores"])
+        has_cmp_kv=cfg["scenario"] >= 2, aic_core_num=cfg["cores"],
+        kv_cache_dtype="fp8_ds_mla")
     dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
     fp8_qk = qk == "fp8"
     out, lse = sparse_attn_sharedkv(**dev, metadata=md.cuda(), return_softmax_lse=True,

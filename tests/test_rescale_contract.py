@@ -133,26 +133,40 @@ def test_split_pieces_merge_like_the_closed_form():
 
 
 def test_fp16_partials_keep_their_scale():
-    # the kernels' split-KV partial format (fp16_partial): rows below 2^15 are plain
-    # fp16 of the value; larger rows (bf16 caches can hold values up to ~3e38) are
-    # scaled by a power of two into [2^14, 2^15) and stay finite, with fp16's
-    # relative precision against the row's largest value
+    # the kernels' split-KV partial format (fp16_partial): every row is scaled by a
+    # power of two that puts its largest |value| into [2^14, 2^15), up or down, so a
+    # row keeps fp16's relative precision against its largest value at any
+    # magnitude a bf16 cache can produce (~1e-38 .. 3e38), and stays finite
     from oracle.kernel_order import fp16_partial
     g = torch.Generator().manual_seed(3)
-    small = torch.randn(8, 512, generator=g) * 100.0
-    assert torch.equal(fp16_partial(small), small.to(torch.float16).to(torch.float32))
-    for mag in (2.0 ** 15, 2.0 ** 15 * 1.999, 1e6, 3e38):
+    for mag in (2.0 ** -130, 2.0 ** -112, 1e-30, 2.0 ** -24, 1e-8, 1e-3, 1.0, 100.0, 2.0 ** 15,
+                2.0 ** 15 * 1.999, 1e6, 3e38):
         o = torch.randn(4, 512, generator=g)
         o = o / o.abs().amax(dim=1, keepdim=True) * mag
         o = o.clamp(-3.3e38, 3.3e38)
         r = fp16_partial(o)
         assert torch.isfinite(r).all()
         m = o.abs().amax(dim=1, keepdim=True)
-        # scaled into [2^14, 2^15), where fp16's half spacing is 8: every element
-        # within 2^-11 of the row max, the row max itself within 2^-12 relative
-        assert ((r - o).abs() <= m * 2.0 ** -11).all(), mag
-        assert ((r.abs().amax(dim=1, keepdim=True) - m).abs() <= m * 2.0 ** -12).all(), mag
-    # NaN elements stay NaN and do not pick the scale; infinities stay infinite
+        # scaled into [2^14, 2^15), where fp16's half spacing is 8: every element,
+        # the row max included, within 2^-11 of the row max (below 2^-112 the scale
+        # stops at 2^126 and the spacing is relative to 2^-112)
+        tol = torch.maximum(m, torch.full_like(m, 2.0 ** -112))
+        assert ((r - o).abs() <= tol * 2.0 ** -11).all(), mag
+        assert ((r.abs().amax(dim=1, keepdim=True) - m).abs() <= tol * 2.0 ** -11).all(), mag
+    # the scale itself: m = 1.5 * 2^-20 is stored as fp16 of m * 2^34 (= 1.5 * 2^14, exact)
+    o = torch.zeros(1, 8)
+    o[0, 0] = 1.5 * 2.0 ** -20
+    o[0, 1] = 2.0 ** -40  # 2^-6 after scaling: a normal fp16, kept exactly
+    assert torch.equal(fp16_partial(o), o)
+    # a one-sided rule (rows below 2^15 left unscaled, as fp16 subnormals) fails the
+    # small rows: 2^-24 * 1.3 would be rounded to fp16's subnormal spacing 2^-24
+    small = torch.full((1, 4), 1.3 * 2.0 ** -24)
+    one_sided = small.to(torch.float16).to(torch.float32)
+    assert (one_sided - small).abs().max() > small.abs().max() * 2.0 ** -11
+    assert ((fp16_partial(small) - small).abs() <= small.abs().max() * 2.0 ** -11).all()
+    # an all-zero row stays zero; NaN elements stay NaN and do not pick the scale;
+    # infinities stay infinite
+    assert torch.equal(fp16_partial(torch.zeros(2, 8)), torch.zeros(2, 8))
     o = torch.ones(2, 8) * 40000.0
     o[0, 3] = float("nan")
     o[1, 2] = float("inf")
