@@ -267,8 +267,11 @@ def main():
         return sorted(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(k))
 
     attn_ms = per_launch(1)
-    has_merge = preps[0].args.num_fd > 0
-    merge_ms = per_launch(2) if has_merge else [0.0] * k  # no split item: no merge kernel
+    # split items are merged by the merge kernel, or inside the attention kernel
+    # (native rows): then the attention launch includes the merge
+    merge_in_attn = preps[0].merge_in_kernel and not sets[0].get("kv_cache_dtype")
+    has_merge = preps[0].args.num_fd > 0 and not merge_in_attn
+    merge_ms = per_launch(2) if has_merge else [0.0] * k  # no merge kernel
     attn_avg = sum(attn_ms) / k
     merge_avg = sum(merge_ms) / k
     srt = attn_ms
@@ -335,6 +338,9 @@ def main():
                            "p50": round(srt[k // 2] * 1e3, 2),
                            "p90": round(srt[(9 * k) // 10] * 1e3, 2)},
         "merge_kernel_us": round(merge_avg * 1e3, 2),
+        "split_items_merged": ("in the attention kernel" if merge_in_attn and
+                               preps[0].args.num_fd > 0 else
+                               "by the merge kernel" if has_merge else "no split items"),
         "host_wall_us_per_step": round(wall / k * 1e6, 2),
         "timing": "value/ms_per_step: K whole calls between two events; attn_kernel_us and "
                   "merge_kernel_us: events around each of K separate launches",

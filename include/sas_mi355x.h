@@ -79,7 +79,8 @@ extern "C" {
 
 /* Host-side scheduler (no GPU needed). Fills meta_out[SAS_META_SIZE].
  * act_q[b]: query rows of batch b; act_kv[b]: raw KV length of batch b.
- * m_base: heads per item (32 when num_heads <= 32, else 64).
+ * m_base: heads per item: 32 when num_heads <= 32, 64 up to 64 heads and for fp8 rows;
+ * above 64 heads on native rows 64 or 128 (one item per token: the 128-head kernel).
  * num_cores: workgroups to balance over (<= SAS_AIC_CORE_NUM).
  * s2_base: positions per schedulable block (multiple of 32).
  * min_split_blocks: an item is split across workgroups only into pieces of at
@@ -114,8 +115,8 @@ int sas_metadata_build_device(int32_t* meta, int batch, const int32_t* act_q,
 
 /* Bytes of split-KV partial workspace for a schedule:
  * num_partial_slots * m_base * (2 * head_dim_v + 8): the partials [slot][head][head_dim_v]
- * as fp16 (acc / l times a power-of-two scale that keeps the row's largest |value|
- * below 2^15; 1 for rows below that), then [slot][head] fp32 lse and [slot][head]
+ * as fp16 (acc / l times the power of two that puts the row's largest |value| into
+ * [2^14, 2^15); 1 for an all-zero row), then [slot][head] fp32 lse and [slot][head]
  * fp32 inverse scales. */
 int64_t sas_workspace_bytes(int num_partial_slots, int m_base, int head_dim_v);
 
@@ -186,10 +187,26 @@ typedef struct SasAttnArgs {
   int32_t phases;
   /* row format of ori_kv and cmp_kv: SAS_KV_NATIVE or SAS_KV_FP8_DS_MLA */
   int32_t kv_format;
+  /* Split-KV merge inside the attention kernel (no reference counterpart: the reference
+   * merges in a separate stage, metadata.py:925-954). NULL: the merge kernel runs after
+   * the attention kernel, as in the reference. Otherwise SAS_MERGE_SYNC_WORDS arrival
+   * counters (device memory, 8-byte aligned) that are zero before the call: each piece
+   * of a split item adds its block count to its item's counter after storing its
+   * partial, and the piece that completes the count merges the item's partials into
+   * out and lse at once, so the merge kernel is not launched (the merge phase enqueues
+   * nothing). The completing piece returns the counter to zero, so a buffer zeroed once
+   * stays usable; calls that may overlap (other streams, graphs replayed concurrently)
+   * need distinct buffers. Results are bit-identical to the merge kernel's. Native
+   * cache rows only (not with SAS_PHASE_PIPELINED); fp8 rows ignore it and run the
+   * merge kernel. */
+  uint64_t* merge_sync;
 } SasAttnArgs;
 
-/* Launch the attention kernel and, when num_fd > 0, the split-KV merge kernel on
- * `stream` (a hipStream_t). Asynchronous; no allocation, no host synchronisation. */
+#define SAS_MERGE_SYNC_WORDS (2 * SAS_AIC_CORE_NUM) /* uint64 counters: one per partial slot */
+
+/* Launch the attention kernel and, when num_fd > 0 and the merge is not done inside
+ * the attention kernel (merge_sync), the split-KV merge kernel on `stream` (a
+ * hipStream_t). Asynchronous; no allocation, no host synchronisation. */
 int sas_attention_launch(const SasAttnArgs* args, void* stream);
 
 /* Allocation-free variant of sas_attention_launch (no counterpart in the reference:

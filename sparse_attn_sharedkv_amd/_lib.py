@@ -36,6 +36,7 @@ FP8_ROW_BYTES = 656
 SAS_PHASE_PIPELINED = 4        # SasAttnArgs.phases bit: native rows through the pipelined kernel
 SAS_PHASE_FP8_QK = 8           # SasAttnArgs.phases bit: fp8 rows, Q·Kᵀ on fp8 MFMA (e4m3 queries)
 SCHED_DEVICE = -1             # SasAttnArgs.num_fd: schedule summary read on the device
+MERGE_SYNC_WORDS = 2 * AIC_CORE_NUM  # SasAttnArgs.merge_sync: uint64 arrival counters
 DEV_SCHED_MAX_BATCH = 4096
 DEV_SCHED_MAX_ITEMS = 16384
 
@@ -82,6 +83,7 @@ class SasAttnArgs(ctypes.Structure):
         ("m_base", ctypes.c_int32),
         ("phases", ctypes.c_int32),
         ("kv_format", ctypes.c_int32),
+        ("merge_sync", ctypes.c_void_p),
     ]
 
 

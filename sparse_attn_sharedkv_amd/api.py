@@ -35,7 +35,8 @@ import torch
 from . import _lib
 from .metadata import (AIC_CORE_NUM, DEFAULT_CORE_NUM, DEFAULT_S2_BASE,  # noqa: F401
                        SAS_META_SIZE,
-                       build_metadata, build_metadata_device, config_row, m_base_for)
+                       build_metadata, build_metadata_device, config_row, m_base_for,
+                       m_base_valid)
 
 DEFAULT_BLOCK_I = 128  # kernel.py:65, kept for callers that import it
 SUPPORTED_HEAD_DIMS = (512, 576)
@@ -73,15 +74,16 @@ class Prepared:
     bsnd_shape: Optional[tuple] = None
     device: Optional[torch.device] = None
     phase_bits: int = 0    # kernel-form bits every launch of this call carries (SAS_PHASE_FP8_QK)
+    merge_in_kernel: bool = True  # split items merged by their last piece (SasAttnArgs.merge_sync)
 
 
 @functools.lru_cache(maxsize=64)
 def _cached_schedule(act_q: tuple, act_kv: tuple, num_heads: int, ori_win_left: int,
                      scenario: int, cmp_ratio: int, topk: int, core_num: int,
-                     fp8: bool) -> torch.Tensor:
+                     fp8: bool, m_base: Optional[int] = None) -> torch.Tensor:
     return build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads,
                           ori_win_left=ori_win_left, scenario=scenario, cmp_ratio=cmp_ratio,
-                          cmp_topk=topk, core_num=core_num, fp8=fp8)
+                          cmp_topk=topk, core_num=core_num, fp8=fp8, m_base=m_base)
 
 
 # Schedules built by the on-device scheduler for calls without ``metadata``: one
@@ -115,6 +117,30 @@ def _schedule_buffer(dev: torch.device) -> torch.Tensor:
     return buf
 
 
+# Arrival counters of the split-KV merge done inside the attention kernel
+# (SasAttnArgs.merge_sync): zero at rest, one buffer per (device, stream) so that
+# calls on different streams never share one; a call captured into a HIP graph
+# gets a buffer of its own (zeroed by a fill kernel recorded in the graph), kept
+# for the life of the process.
+_MERGE_SYNC: dict = {}
+_CAPTURED_MERGE_SYNC: list = []
+
+
+def _merge_sync_buffer(dev: torch.device, st: torch.cuda.Stream) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        buf = torch.zeros(_lib.MERGE_SYNC_WORDS, dtype=torch.int64, device=dev)
+        with _DEVICE_SCHEDULES_LOCK:
+            _CAPTURED_MERGE_SYNC.append(buf)
+        return buf
+    key = (dev.index, st.cuda_stream)
+    with _DEVICE_SCHEDULES_LOCK:
+        buf = _MERGE_SYNC.get(key)
+        if buf is None:
+            buf = torch.zeros(_lib.MERGE_SYNC_WORDS, dtype=torch.int64, device=dev)
+            _MERGE_SYNC[key] = buf
+    return buf
+
+
 def _ptr(t: Optional[torch.Tensor]):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
@@ -134,7 +160,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             schedule: Optional[str] = None,
             fp8_qk: bool = False,
             _stream_schedule: bool = False,
-            _pipelined: bool = False) -> Prepared:
+            _pipelined: bool = False, _separate_merge: bool = False,
+            _m_base: Optional[int] = None) -> Prepared:
     """Validate and stage one call (host work of api.py:186-384) without launching.
 
     ``schedule``: ``"host"`` reads the lengths back and schedules on the CPU (the
@@ -146,7 +173,10 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     buffer for the current stream and is kept when unchanged; otherwise every
     prepared call schedules into a buffer of its own. ``_pipelined`` (tests): native
     rows run through the kernel fp8 rows use (``SAS_PHASE_PIPELINED``, items of at
-    most 64 heads), for bitwise comparisons with the fp8 path.
+    most 64 heads), for bitwise comparisons with the fp8 path. ``_separate_merge``
+    (tests, timing): split items are merged by the merge kernel after the attention
+    kernel instead of inside it. ``_m_base`` (tests, timing): heads per item instead
+    of ``m_base_for``'s choice (a call with its own ``metadata`` uses the metadata's).
     """
     del seqused_q  # API-parity placeholder (api.py:186)
     assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
@@ -221,6 +251,9 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     fp8_rows = kv_fmt == _lib.KV_FP8_DS_MLA
     # items of at most 64 heads: fp8 rows and the pipelined kernel (m_base_for)
     item64 = fp8_rows or _pipelined
+    m_base = m_base_for(int(n1), item64, nb) if _m_base is None else int(_m_base)
+    if not m_base_valid(int(n1), item64, m_base):
+        raise ValueError(f"no kernel for items of {m_base} heads at {n1} heads")
     row_width = _lib.FP8_ROW_BYTES if fp8_rows else d
     dv = (512 if fp8_rows else d) if head_dim_v is None else int(head_dim_v)
     if n2 != 1 or ori_kv.shape[2] != 1 or ori_kv.shape[-1] != row_width:
@@ -290,7 +323,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                 batch=nb, act_q=act_q_d, act_kv=seqused, num_heads=int(n1),
                 ori_win_left=int(ori_win_left), scenario=scenario, cmp_ratio=cmp_ratio_eff,
                 cmp_topk=int(k), core_num=int(core_num),
-                out=_schedule_buffer(dev) if _stream_schedule else None, fp8=item64)
+                out=_schedule_buffer(dev) if _stream_schedule else None, fp8=item64,
+                m_base=m_base)
         else:
             metadata_dev = metadata.to(device=dev, dtype=i32).reshape(SAS_META_SIZE).contiguous()
         # capacities; the kernels read the schedule's own summary on the GPU. A
@@ -300,17 +334,17 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
         # for the most partial pieces such a schedule can have (two per core).
         cap = int(core_num) if metadata is None else AIC_CORE_NUM
         cfg = dict(num_fa=cap, num_fd=_lib.SCHED_DEVICE, num_partial_slots=2 * cap,
-                   s2_base=DEFAULT_S2_BASE, m_base=m_base_for(n1, item64))
+                   s2_base=DEFAULT_S2_BASE, m_base=m_base)
     elif metadata is None:
         kv_host = tuple(int(x) for x in seqused_kv.to(torch.int32).cpu().tolist())
         md = _cached_schedule(tuple(act_q), kv_host, int(n1), int(ori_win_left), scenario,
-                              cmp_ratio_eff, int(k), int(core_num), item64)
+                              cmp_ratio_eff, int(k), int(core_num), item64, m_base)
         cfg = config_row(md)
         metadata_dev = md.to(dev, non_blocking=True)
     else:
         metadata_dev = metadata.to(dev).to(torch.int32).reshape(SAS_META_SIZE).contiguous()
         cfg = config_row(metadata)  # host read of the schedule summary row
-        assert cfg["num_heads"] == n1 and cfg["m_base"] == m_base_for(n1, item64), (
+        assert cfg["num_heads"] == n1 and m_base_valid(n1, item64, cfg["m_base"]), (
             "metadata was built for a different head count or cache row format "
             "(fp8 cache rows: sparse_attn_sharedkv_metadata(..., kv_cache_dtype='fp8_ds_mla'))")
 
@@ -364,7 +398,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     return Prepared(args=a, keep=keep, out=out, lse=lse, layout_q=layout_q,
                     bsnd_shape=None if layout_q == "TND" else (nb, total // max(nb, 1), n1, dv),
                     device=dev, phase_bits=(_lib.SAS_PHASE_FP8_QK if fp8_qk else 0) |
-                    (_lib.SAS_PHASE_PIPELINED if _pipelined else 0))
+                    (_lib.SAS_PHASE_PIPELINED if _pipelined else 0),
+                    merge_in_kernel=not _separate_merge)
 
 
 def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: int = 0) -> None:
@@ -376,6 +411,13 @@ def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: i
     lib = _lib.load()
     st = stream if stream is not None else torch.cuda.current_stream(prep.device)
     prep.args.phases = int(phases) | prep.phase_bits
+    if prep.merge_in_kernel and prep.args.workspace:
+        sync = _merge_sync_buffer(prep.device, st)
+        prep.args.merge_sync = sync.data_ptr()
+        if not any(t is sync for t in prep.keep):
+            prep.keep.append(sync)
+    else:
+        prep.args.merge_sync = None
     rc = lib.sas_attention_launch(ctypes.byref(prep.args), ctypes.c_void_p(st.cuda_stream))
     if rc != _lib.SAS_OK:
         raise RuntimeError(_lib.last_error())

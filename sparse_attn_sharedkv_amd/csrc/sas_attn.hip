@@ -261,6 +261,187 @@ __device__ inline float* partial_lse(const SasAttnArgs& a, int mb, int dv) {
   return (float*)((char*)a.workspace + (size_t)a.num_partial_slots * mb * dv * 2);
 }
 
+// ---------------------------------------------------------------------------
+// Split-KV merge inside the attention kernel (SasAttnArgs.merge_sync)
+// ---------------------------------------------------------------------------
+// The pieces of a split item sit in consecutive FA rows and take consecutive
+// partial slots in block order (both schedulers number slots in core order).
+// A row whose first item starts at a block > 0 continues an item begun in the
+// rows before it; its piece index is 1 + the number of rows just before it that
+// also start inside that item. Lane l looks at row fa_row - 1 - l (the first 64
+// rows; continued_piece_index walks further for items of more pieces).
+struct ContScan {
+  int b, m, j;  // start cursor of row fa_row - 1 - lane (b = -1: no such row)
+};
+__device__ inline ContScan cont_scan_load(const SasAttnArgs& a, int fa_row, int lane) {
+  const int r = fa_row - 1 - lane;
+  if (r < 0) return {-1, 0, 0};
+  const int32_t* p = a.metadata + (size_t)r * SAS_FA_METADATA_SIZE;
+  return {p[1], p[2], p[3]};
+}
+__device__ inline int continued_piece_index(const SasAttnArgs& a, int fa_row, int b, int m,
+                                            ContScan first) {
+  const int lane = threadIdx.x & 63;
+  int k = 1;
+  ContScan c = first;
+  for (int r0 = fa_row - 1;; r0 -= 64) {
+    const bool cont = c.b == b && c.m == m && c.j > 0;
+    const uint64_t stop = ~(uint64_t)__ballot(cont);
+    if (stop != 0) return k + __builtin_ctzll(stop);
+    k += 64;
+    c = cont_scan_load(a, r0 - 63, lane);  // rows r0 - 64 - lane
+  }
+}
+
+// Partials that another workgroup merges are written and read with agent-scope
+// coherent accesses (sc1: through to the device's coherence point, past the
+// per-XCD L2 caches), so the hand-over needs no cache-wide writeback or
+// invalidate: a piece waits for its stores to complete, then counts itself in;
+// the merging piece reads after it has seen the count.
+__device__ inline __amdgpu_buffer_rsrc_t partial_rsrc(const SasAttnArgs& a, int mb, int dv) {
+  const int bytes = a.num_partial_slots * mb * (2 * dv + 8);  // the workspace (< 2^31)
+  return __builtin_amdgcn_make_buffer_rsrc(a.workspace, 0, bytes, 0x00020000);
+}
+constexpr int CPOL_SC1 = 16;  // buffer instruction cache policy: agent-scope coherent
+__device__ inline void partial_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, i32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, CPOL_SC1);
+}
+__device__ inline void partial_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(v), r, (int)off, 0, CPOL_SC1);
+}
+
+// Arrival of a piece whose partial every thread of the workgroup has stored
+// (with partial_store16 / partial_store4): adds the piece's blocks (low 32 bits)
+// and, from the item's final piece, the piece count (high 32 bits) to the item's
+// counter merge_sync[slot0]. Returns the piece count to the piece that completes
+// the item's blocks (it merges the item and has returned the counter to zero),
+// 0 to the others.
+__device__ inline int split_arrive(const SasAttnArgs& a, int slot0, int slot, int blocks,
+                                   bool final_piece, int nblk, int* lds_word) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are done
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned long long add =
+        (unsigned long long)(uint32_t)blocks |
+        (final_piece ? (unsigned long long)(uint32_t)(slot - slot0 + 1) << 32 : 0ull);
+    unsigned long long* c = (unsigned long long*)a.merge_sync + slot0;
+    const unsigned long long tot =
+        __hip_atomic_fetch_add(c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+    int r = 0;
+    if ((uint32_t)tot == (uint32_t)nblk) {
+      r = (int)(tot >> 32);
+      __hip_atomic_store(c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *lds_word = r;
+  }
+  __syncthreads();
+  return *lds_word;
+}
+
+// Merge of split item (token tok, head block hb; pieces in slots slot0 ..
+// slot0 + npc - 1) by a workgroup of NW waves: wave w takes heads
+// [w * MB / NW, +MB / NW) of the block in groups of G, lane l dims 8 l .. 8 l + 7
+// of each; the loads of PB pieces are in flight together. The arithmetic is
+// merge_task's (below) operation for operation (o starts at -0, so the first
+// fused multiply-add rounds as merge_task's first product), so out and lse are
+// bit-identical to the merge kernel's.
+template <int DV, typename T, int MB, int NW>
+__device__ void merge_item_here(const SasAttnArgs& a, int tok, int hb, int slot0, int npc) {
+  constexpr int HPW = MB / NW;
+  constexpr int G = HPW < 8 ? HPW : 8;  // heads per group
+  constexpr int PB = 2;                 // pieces per batch of loads
+  static_assert(DV == 512 && MB % NW == 0 && HPW % G == 0 && HPW <= 64, "merge layout");
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nh = min(MB, a.num_heads - hb * MB);
+  const int hw0 = w * HPW;
+  if (hw0 >= nh) return;
+  const __amdgpu_buffer_rsrc_t rs = partial_rsrc(a, MB, DV);
+  const uint32_t lse_off = (uint32_t)a.num_partial_slots * MB * DV * 2;  // bytes
+  const uint32_t inv_off = lse_off + (uint32_t)a.num_partial_slots * MB * 4;
+  auto ldf = [&](uint32_t off) -> float {
+    return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, CPOL_SC1));
+  };
+  // lse of head hw0 + lane (lanes < HPW; the others repeat head hw0)
+  const int hk = hw0 + (lane < HPW && hw0 + lane < nh ? lane : 0);
+  const int hq = hb * MB + hk;
+  const float sink = a.sinks[hq];
+  auto plse = [&](int i) { return ldf(lse_off + ((uint32_t)(slot0 + i) * MB + hk) * 4); };
+  auto pinv = [&](int i) { return ldf(inv_off + ((uint32_t)(slot0 + i) * MB + hk) * 4); };
+  constexpr int MAXL = 8;
+  float lv[MAXL];
+#pragma unroll
+  for (int i = 0; i < MAXL; ++i) lv[i] = plse(i < npc ? i : npc - 1);
+  float mx = fmaxf(sink, lv[0]);
+#pragma unroll
+  for (int i = 1; i < MAXL; ++i)
+    if (i < npc) mx = fmaxf(mx, lv[i]);
+  for (int i = MAXL; i < npc; ++i) mx = fmaxf(mx, plse(i));
+  float l = -INFINITY;
+  if (mx != -INFINITY) {
+    float tot = __expf(sink - mx) + __expf(lv[0] - mx);
+#pragma unroll
+    for (int i = 1; i < MAXL; ++i)
+      if (i < npc) tot += __expf(lv[i] - mx);
+    for (int i = MAXL; i < npc; ++i) tot += __expf(plse(i) - mx);
+    l = mx + __logf(tot);
+  }
+  // the weights of the wave's heads (lane k: head hw0 + k) for piece i
+  auto wlane = [&](int i) -> float {
+    const float li = plse(i);  // (lv[i] again: loaded beside the piece's data)
+    return ((l == -INFINITY || li == -INFINITY) ? 0.0f : __expf(li - l)) * pinv(i);
+  };
+  const bool tok_ok = tok >= 0 && tok < a.total_tokens;
+  for (int g0 = 0; g0 < HPW; g0 += G) {
+    f32x4 o[G][2];
+#pragma unroll
+    for (int k = 0; k < G; ++k) o[k][0] = o[k][1] = (f32x4){-0.0f, -0.0f, -0.0f, -0.0f};
+    for (int i0 = 0; i0 < npc; i0 += PB) {
+      i32x4 v[PB][G];
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        const int i = i0 + j < npc ? i0 + j : npc - 1;  // clamped: every load unconditional
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+          const int h = hw0 + g0 + k < nh ? hw0 + g0 + k : nh - 1;
+          const uint32_t off = (((uint32_t)(slot0 + i) * MB + h) * DV + 8 * lane) * 2;
+          v[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, CPOL_SC1);
+        }
+      }
+      float wj[PB];
+#pragma unroll
+      for (int j = 0; j < PB; ++j) wj[j] = wlane(i0 + j < npc ? i0 + j : npc - 1);
+      __builtin_amdgcn_sched_barrier(0);  // every load of the batch issued before the first use
+#pragma unroll
+      for (int j = 0; j < PB; ++j) {
+        if (i0 + j >= npc) break;
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+          const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj[j]), g0 + k));
+          typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+          const h16x8 x = __builtin_bit_cast(h16x8, v[j][k]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            o[k][e >> 2][e & 3] = __builtin_fmaf(wk, (float)x[e], o[k][e >> 2][e & 3]);
+        }
+      }
+    }
+    if (tok_ok) {
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        if (hw0 + g0 + k >= nh) break;
+        T* orow = (T*)a.out + ((size_t)tok * a.num_heads + hb * MB + hw0 + g0 + k) * DV + 8 * lane;
+        const i16x8 pk = {MfmaOps<T>::from_f32(o[k][0][0]), MfmaOps<T>::from_f32(o[k][0][1]),
+                          MfmaOps<T>::from_f32(o[k][0][2]), MfmaOps<T>::from_f32(o[k][0][3]),
+                          MfmaOps<T>::from_f32(o[k][1][0]), MfmaOps<T>::from_f32(o[k][1][1]),
+                          MfmaOps<T>::from_f32(o[k][1][2]), MfmaOps<T>::from_f32(o[k][1][3])};
+        *(i16x8*)orow = pk;
+      }
+    }
+  }
+  if (tok_ok && lane < HPW && hw0 + lane < nh) a.lse[(size_t)tok * a.num_heads + hq] = l;
+}
+
 // fp8 cache rows (SAS_KV_FP8_DS_MLA): eight e4m3 values (one 8-byte word) times
 // their block scale, each product rounded to bf16 (v_cvt_pk_f32_fp8 decodes OCP
 // e4m3 exactly; v_mul_f32 and v_cvt_pk_bf16_f32 round to nearest even).
@@ -384,6 +565,7 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   __shared__ __attribute__((aligned(16))) f32x4 xbuf[2][NW][4][64];  // partial Sᵀ of each wave, per tile of a pair
   __shared__ uint32_t rowid[RCH];
   __shared__ uint32_t tmask[RCH / TILE];
+  __shared__ int merge_word;    // split_arrive's answer to the workgroup
   __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
 
   const int tid = threadIdx.x;
@@ -428,6 +610,11 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
   const int b_end = fa[4], s_end = fa[5], j_end = fa[6];
   int slot = fa[7];
   const uint32_t kv_base = (uint32_t)(uintptr_t)kv_lds;
+  // in-kernel merge: the start cursors of the rows before this one, when its
+  // first item continues a split item (loaded beside the lengths)
+  const bool merge_here = a.merge_sync != nullptr && a.workspace != nullptr;
+  ContScan cscan = {-1, 0, 0};
+  if (merge_here && j_start > 0) cscan = cont_scan_load(a, fa_row, lane);
 
   const char* ori_kv = (const char*)a.ori_kv;
   const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
@@ -444,6 +631,8 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
     lane_qp = a.q_prefix[lb];
   }
   if (tid < 2) first_neg[tid] = INT32_MAX;
+  // piece index of the first item when it continues a split item
+  const int cont_k = (merge_here && j_start > 0) ? continued_piece_index(a, fa_row, b, m, cscan) : 0;
   __syncthreads();
 
   // Sinks of this lane's head in the (at most two) head blocks of an item,
@@ -1076,16 +1265,43 @@ __global__ __launch_bounds__(128 * NHG) void attn2_kernel(const SasAttnArgs a) {
             *(i16x4*)(stg + hl_e * SROW + dv * 2) = v;
           }
         __syncthreads();
-        char* wbase = (char*)a.workspace + (size_t)slot * MB * DV * 2;
-        for (int c = tid_e; c < nh * CPR; c += NT) {
-          const int h = c / CPR, c16 = c - h * CPR;
-          *(i16x8*)(wbase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
+        const float lse_piece = empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
+        if (merge_here) {
+          // read by another workgroup in this launch: agent-coherent stores
+          const __amdgpu_buffer_rsrc_t rs = partial_rsrc(a, MB, DV);
+          const uint32_t base = (uint32_t)slot * MB * DV * 2;
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            partial_store16(rs, base + (uint32_t)(h * DV * 2 + c16 * 16),
+                            *(const i32x4*)(stg + h * SROW + c16 * 16));
+          }
+          if (dh == 0 && hl == 0 && head_ok) {
+            const uint32_t lo = (uint32_t)a.num_partial_slots * MB * DV * 2;
+            partial_store4(rs, lo + ((uint32_t)slot * MB + hl_e) * 4, lse_piece);
+            partial_store4(rs, lo + ((uint32_t)(a.num_partial_slots + slot) * MB + hl_e) * 4,
+                           ps.inv);
+          }
+        } else {
+          char* wbase = (char*)a.workspace + (size_t)slot * MB * DV * 2;
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            *(i16x8*)(wbase + (size_t)h * DV * 2 + c16 * 16) =
+                *(const i16x8*)(stg + h * SROW + c16 * 16);
+          }
+          if (dh == 0 && hl == 0 && head_ok) {
+            float* wl = partial_lse(a, MB, DV);
+            wl[(size_t)slot * MB + hl_e] = lse_piece;
+            wl[(size_t)(a.num_partial_slots + slot) * MB + hl_e] = ps.inv;
+          }
         }
-        if (dh == 0 && hl == 0 && head_ok) {
-          float* wl = partial_lse(a, MB, DV);
-          wl[(size_t)slot * MB + hl_e] = empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
-          wl[(size_t)(a.num_partial_slots + slot) * MB + hl_e] = ps.inv;
-        }
+      }
+    }
+    if (partial && merge_here) {
+      // the piece that completes the item merges it (bit-identical to merge_kernel)
+      const int slot0 = (first_item && j_start > 0) ? slot - cont_k : slot;
+      if (slot0 >= 0 && slot < a.num_partial_slots && slot0 < SAS_MERGE_SYNC_WORDS) {
+        const int npc = split_arrive(a, slot0, slot, bhi - blo, bhi == nblk, nblk, &merge_word);
+        if (npc > 0) merge_item_here<DV, T, MB, NW>(a, tok, hb, slot0, npc);
       }
     }
     if (partial) ++slot;
@@ -2109,10 +2325,9 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
     if (npc > 1) {
       const float w1 = weight(l1) * s1;
 #pragma unroll
-      for (int k = 0; k < PER; ++k) {
-        o[k][0] += w1 * v1[k][0]; o[k][1] += w1 * v1[k][1];
-        o[k][2] += w1 * v1[k][2]; o[k][3] += w1 * v1[k][3];
-      }
+      for (int k = 0; k < PER; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[k][e] = __builtin_fmaf(w1, v1[k][e], o[k][e]);
     }
   } else {
     // more pieces: their data in batches of PB with all loads of a batch in
@@ -2161,8 +2376,8 @@ __device__ __forceinline__ void merge_task(const SasAttnArgs& a, int task) {
           if (i0 + i == 0) {
             o[k] = (f32x4){wi * vb[i][k][0], wi * vb[i][k][1], wi * vb[i][k][2], wi * vb[i][k][3]};
           } else {
-            o[k][0] += wi * vb[i][k][0]; o[k][1] += wi * vb[i][k][1];
-            o[k][2] += wi * vb[i][k][2]; o[k][3] += wi * vb[i][k][3];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[k][e] = __builtin_fmaf(wi, vb[i][k][e], o[k][e]);
           }
         }
       }
@@ -2236,7 +2451,11 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   const bool dev = a.num_fd == SAS_SCHED_DEVICE;
-  if ((phases & 2) && (a.num_fd > 0 || dev)) {
+  // the native-row kernels (128-head and one-wave-per-SIMD) merge split items
+  // themselves when given arrival counters
+  const bool merged_in_attn = KVF == SAS_KV_NATIVE && !(a.phases & SAS_PHASE_PIPELINED) &&
+                              a.merge_sync != nullptr && a.workspace != nullptr;
+  if ((phases & 2) && (a.num_fd > 0 || dev) && !merged_in_attn) {
     const int groups = (a.m_base + MERGE_HPB - 1) / MERGE_HPB;  // head groups per task (upper bound)
     const int tasks = dev ? (a.num_fa < 256 ? a.num_fa : 256) : a.num_fd;  // columns; tasks strided
     const int cols = (tasks + 7) / 8 * 8;  // a multiple of the 8 XCDs
@@ -2297,9 +2516,10 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
   // rows run through the pipelined kernel (SAS_PHASE_PIPELINED)
   const bool item64 = a->kv_format == SAS_KV_FP8_DS_MLA || (a->phases & SAS_PHASE_PIPELINED);
   const int want_mb = a->num_heads <= 32 ? 32 : (a->num_heads <= 64 || item64) ? 64 : 128;
-  if (a->m_base != want_mb) {
+  // native rows above 64 heads may also be scheduled in 64-head items (two per token)
+  if (a->m_base != want_mb && !(want_mb == 128 && a->m_base == 64)) {
     set_error("sas_attention_launch: m_base must be 32 for <= 32 heads, 64 for <= 64 heads "
-              "(or fp8 rows, or SAS_PHASE_PIPELINED), else 128");
+              "(or fp8 rows, or SAS_PHASE_PIPELINED), else 128 or 64");
     return SAS_E_INVALID;
   }
   if (a->scenario < 1 || a->scenario > 3 || (a->scenario >= 2 && (!a->cmp_kv ||
@@ -2321,6 +2541,12 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
       a->num_fd > SAS_AIV_CORE_NUM || a->s2_base < 32 || (a->s2_base % 32) != 0 ||
       ((a->num_fd > 0 || dev_sched) && (!a->workspace || a->num_partial_slots < 1))) {
     set_error("sas_attention_launch: inconsistent schedule");
+    return SAS_E_INVALID;
+  }
+  if (a->merge_sync && (((uintptr_t)a->merge_sync & 7) != 0 ||
+                        a->num_partial_slots > SAS_MERGE_SYNC_WORDS)) {
+    set_error("sas_attention_launch: merge_sync must be 8-byte aligned and the schedule "
+              "within SAS_MERGE_SYNC_WORDS partial slots");
     return SAS_E_INVALID;
   }
   if (a->ori_block_num < 1 || a->ori_block_size < 1 || a->ori_table_len < 1 || a->batch < 0 ||
@@ -2400,12 +2626,15 @@ extern "C" int sas_attention_launch_noalloc(const SasAttnArgs* a, void* stream) 
     sas::set_error("sas_attention_launch_noalloc: null args");
     return SAS_E_INVALID;
   }
+  // the last SAS_MERGE_SYNC_WORDS words of the scratch array hold the in-kernel
+  // merge's arrival counters (zero when the library is loaded, zero after each call)
+  constexpr int64_t SYNC_BYTES = (int64_t)SAS_MERGE_SYNC_WORDS * 8;
   const int64_t need = sas_workspace_bytes(a->num_partial_slots, a->m_base, a->head_dim_v);
-  if (need > (int64_t)SAS_NOALLOC_SCRATCH_BYTES) {
+  if (need > (int64_t)SAS_NOALLOC_SCRATCH_BYTES - SYNC_BYTES) {
     sas::set_error("sas_attention_launch_noalloc: the schedule's split-KV workspace (" +
                    std::to_string(need) + " bytes for " + std::to_string(a->num_partial_slots) +
                    " partial slots) exceeds the fixed scratch of " +
-                   std::to_string((long long)SAS_NOALLOC_SCRATCH_BYTES) + " bytes");
+                   std::to_string((long long)(SAS_NOALLOC_SCRATCH_BYTES - SYNC_BYTES)) + " bytes");
     return SAS_E_CAPACITY;
   }
   float* ws = nullptr;
@@ -2413,10 +2642,14 @@ extern "C" int sas_attention_launch_noalloc(const SasAttnArgs* a, void* stream) 
   if (rc != SAS_OK) return rc;
   SasAttnArgs b = *a;
   b.workspace = ws;  // the caller's workspace pointer, if any, is not used
+  // a non-null merge_sync asks for the in-kernel merge; its counters are the scratch's
+  b.merge_sync = a->merge_sync
+                     ? (uint64_t*)((char*)ws + SAS_NOALLOC_SCRATCH_BYTES - SYNC_BYTES)
+                     : nullptr;
   return sas_attention_launch(&b, stream);
 }
 
-extern "C" int sas_version(void) { return 111; }
+extern "C" int sas_version(void) { return 112; }
 
 extern "C" int sas_args_struct_size(void) { return (int)sizeof(SasAttnArgs); }
 

@@ -116,6 +116,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   __shared__ uint32_t rowid[RCH];
   __shared__ uint32_t tmask[RCH / TILE];
   __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
+  __shared__ int merge_word;    // split_arrive's answer to the workgroup
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -145,6 +146,11 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   const int b_end = fa[4], s_end = fa[5], j_end = fa[6];
   int slot = fa[7];
   const uint32_t kv_base = (uint32_t)(uintptr_t)kv_lds;
+  // in-kernel merge: the start cursors of the rows before this one, when its
+  // first item continues a split item (loaded beside the lengths)
+  const bool merge_here = a.merge_sync != nullptr && a.workspace != nullptr;
+  ContScan cscan = {-1, 0, 0};
+  if (merge_here && j_start > 0) cscan = cont_scan_load(a, fa_row, lane);
 
   const char* ori_kv = (const char*)a.ori_kv;
   const char* cmp_kv = (const char*)(a.cmp_kv ? a.cmp_kv : a.ori_kv);
@@ -161,6 +167,8 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
     lane_qp = a.q_prefix[lb];
   }
   if (tid < 2) first_neg[tid] = INT32_MAX;
+  // piece index of the first item when it continues a split item
+  const int cont_k = (merge_here && j_start > 0) ? continued_piece_index(a, fa_row, b, m, cscan) : 0;
   __syncthreads();
   // sink of this lane's head (an item holds every head: one head block)
   const float sink_h = hlocal < a.num_heads ? a.sinks[hlocal] : -INFINITY;
@@ -653,16 +661,43 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
           *(i16x4*)(stg + hl_e * SROW + (16 * d + dv_e) * 2) = v;
         }
         __syncthreads();
-        char* wbase = (char*)a.workspace + (size_t)slot * MB * DV * 2;
-        for (int c = tid_e; c < nh * CPR; c += NT) {
-          const int h = c / CPR, c16 = c - h * CPR;
-          *(i16x8*)(wbase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
+        const float lse_piece = empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
+        if (merge_here) {
+          // read by another workgroup in this launch: agent-coherent stores
+          const __amdgpu_buffer_rsrc_t rs = partial_rsrc(a, MB, DV);
+          const uint32_t base = (uint32_t)slot * MB * DV * 2;
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            partial_store16(rs, base + (uint32_t)(h * DV * 2 + c16 * 16),
+                            *(const i32x4*)(stg + h * SROW + c16 * 16));
+          }
+          if (g4 == 0 && head_ok) {
+            const uint32_t lo = (uint32_t)a.num_partial_slots * MB * DV * 2;
+            partial_store4(rs, lo + ((uint32_t)slot * MB + hl_e) * 4, lse_piece);
+            partial_store4(rs, lo + ((uint32_t)(a.num_partial_slots + slot) * MB + hl_e) * 4,
+                           ps.inv);
+          }
+        } else {
+          char* wbase = (char*)a.workspace + (size_t)slot * MB * DV * 2;
+          for (int c = tid_e; c < nh * CPR; c += NT) {
+            const int h = c / CPR, c16 = c - h * CPR;
+            *(i16x8*)(wbase + (size_t)h * DV * 2 + c16 * 16) =
+                *(const i16x8*)(stg + h * SROW + c16 * 16);
+          }
+          if (g4 == 0 && head_ok) {
+            float* wl = partial_lse(a, MB, DV);
+            wl[(size_t)slot * MB + hl_e] = lse_piece;
+            wl[(size_t)(a.num_partial_slots + slot) * MB + hl_e] = ps.inv;
+          }
         }
-        if (g4 == 0 && head_ok) {
-          float* wl = partial_lse(a, MB, DV);
-          wl[(size_t)slot * MB + hl_e] = empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
-          wl[(size_t)(a.num_partial_slots + slot) * MB + hl_e] = ps.inv;
-        }
+      }
+    }
+    if (partial && merge_here) {
+      // the piece that completes the item merges it (bit-identical to merge_kernel)
+      const int slot0 = (first_item && j_start > 0) ? slot - cont_k : slot;
+      if (slot0 >= 0 && slot < a.num_partial_slots && slot0 < SAS_MERGE_SYNC_WORDS) {
+        const int npc = split_arrive(a, slot0, slot, bhi - blo, bhi == nblk, nblk, &merge_word);
+        if (npc > 0) merge_item_here<DV, T, MB, NW>(a, tok, hb, slot0, npc);
       }
     }
     if (partial) ++slot;

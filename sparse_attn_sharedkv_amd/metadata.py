@@ -44,16 +44,38 @@ DEFAULT_MIN_SPLIT_BLOCKS = 2  # never split an item into pieces shorter than 128
 DEFAULT_FD_HEAD_CHUNK = 64    # heads per merge task (a whole 64-head item)
 
 
-def m_base_for(num_heads: int, fp8: bool = False) -> int:
+# Above 64 heads, native rows take items of every head of a token (128) from this
+# many sequences on: with fewer, 128-head items need more pieces per item to fill
+# the 256 workgroups, and their split-KV partials cost more than reading each
+# gathered row once per 64 heads (measured on MI355X: top-k 2048 decode at 64
+# sequences, 62.9 us per call with 64-head items against 67.0 us; 128-head items
+# are ahead from 128 query rows on).
+WIDE_ITEM_MIN_BATCH = 128
+
+
+def m_base_for(num_heads: int, fp8: bool = False, batch: Optional[int] = None) -> int:
     """Heads per schedulable item (the reference's mBaseSize, metadata.py:388).
 
-    32 up to 32 heads and 64 up to 64 heads, as the reference; above 64 heads an
-    item holds all of a token's heads (128) for native bf16 / fp16 rows, whose
-    kernel serves every head of the token from one gathered tile, and stays 64
-    for fp8 cache rows (``fp8=True``)."""
+    32 up to 32 heads and 64 up to 64 heads, as the reference. Above 64 heads an
+    item holds all of a token's heads (128) for native bf16 / fp16 rows when the
+    call has at least ``WIDE_ITEM_MIN_BATCH`` sequences (``batch``; a kernel then
+    serves every head of the token from one gathered tile), else 64; fp8 cache rows
+    (``fp8=True``) keep 64. The rule reads only values both schedulers and every
+    entry point know alike (head count, row format, sequence count)."""
     if num_heads <= 32:
         return 32
-    return 64 if (num_heads <= 64 or fp8) else 128
+    if num_heads <= 64 or fp8 or batch is None or batch < WIDE_ITEM_MIN_BATCH:
+        return 64
+    return 128
+
+
+def m_base_valid(num_heads: int, fp8: bool, m_base: int) -> bool:
+    """Item sizes the kernels accept for a head count and row format."""
+    if num_heads <= 32:
+        return m_base == 32
+    if num_heads <= 64 or fp8:
+        return m_base == 64
+    return m_base in (64, 128)
 
 
 def _is_fp8(kv_cache_dtype) -> bool:
@@ -105,17 +127,21 @@ def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: in
                    ori_win_left: int, scenario: int, cmp_ratio: int, cmp_topk: int,
                    core_num: int = DEFAULT_CORE_NUM, s2_base: int = DEFAULT_S2_BASE,
                    min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
-                   fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK, fp8: bool = False) -> torch.Tensor:
+                   fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK, fp8: bool = False,
+                   m_base: Optional[int] = None) -> torch.Tensor:
     """Run the C++ scheduler; returns an int32 CPU tensor of ``SAS_META_SIZE`` words.
-    ``fp8``: the schedule is for fp8 cache rows (64-head items, ``m_base_for``)."""
+    ``fp8``: the schedule is for fp8 cache rows (64-head items, ``m_base_for``);
+    ``m_base``: the item size (default ``m_base_for``)."""
     lib = _lib.load()
     b = len(act_q)
+    if m_base is None:
+        m_base = m_base_for(int(num_heads), fp8, b)
     out = torch.zeros(SAS_META_SIZE, dtype=torch.int32)
     aq = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_q])
     ak = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_kv])
     i32p = ctypes.POINTER(ctypes.c_int32)
     rc = lib.sas_metadata_build(ctypes.cast(out.data_ptr(), i32p), b, aq, ak, int(num_heads),
-                                m_base_for(int(num_heads), fp8), int(ori_win_left), int(scenario),
+                                int(m_base), int(ori_win_left), int(scenario),
                                 int(cmp_ratio), int(cmp_topk), int(core_num), int(s2_base),
                                 int(min_split_blocks), int(fd_head_chunk))
     if rc < 0:
@@ -168,7 +194,8 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
                           min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
                           fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK,
                           stream: Optional[torch.cuda.Stream] = None,
-                          out: Optional[torch.Tensor] = None, fp8: bool = False) -> torch.Tensor:
+                          out: Optional[torch.Tensor] = None, fp8: bool = False,
+                          m_base: Optional[int] = None) -> torch.Tensor:
     """Run the on-device scheduler (``sas_metadata_build_device``) on the current stream.
 
     ``act_q`` / ``act_kv``: int32 ``[batch]`` tensors on the GPU (``act_q`` None: every
@@ -199,10 +226,12 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
           or not out.is_contiguous()):
         raise ValueError(f"out must be a contiguous int32 [{SAS_META_SIZE}] tensor on {dev}")
     st = stream if stream is not None else torch.cuda.current_stream(dev)
+    if m_base is None:
+        m_base = m_base_for(int(num_heads), fp8, int(batch))
     rc = lib.sas_metadata_build_device(
         ctypes.c_void_p(out.data_ptr()), int(batch),
         ctypes.c_void_p(act_q.data_ptr() if act_q is not None else 0), int(uniform_q),
-        ctypes.c_void_p(act_kv.data_ptr()), int(num_heads), m_base_for(int(num_heads), fp8),
+        ctypes.c_void_p(act_kv.data_ptr()), int(num_heads), int(m_base),
         int(ori_win_left), int(scenario), int(cmp_ratio), int(cmp_topk), int(core_num),
         int(s2_base), int(min_split_blocks), int(fd_head_chunk), int(reuse),
         ctypes.c_void_p(st.cuda_stream))
@@ -262,7 +291,8 @@ def sparse_attn_sharedkv_metadata(
     (or already on) that GPU, without reading them back; the words are the ones
     the host scheduler produces. ``kv_cache_dtype`` (no reference counterpart):
     ``"fp8_ds_mla"`` builds the schedule for calls on fp8 cache rows, whose items
-    hold at most 64 heads (``m_base_for``).
+    hold at most 64 heads. Items hold 32, 64 or 128 heads (``m_base_for``: 128 only
+    for native rows above 64 heads with at least ``WIDE_ITEM_MIN_BATCH`` sequences).
     """
     del cu_seqlens_cmp_kv, head_dim, ori_topk, aiv_core_num
     if num_heads_kv != 1:

@@ -348,3 +348,28 @@ def test_split_partials_of_large_values():
     assert torch.isfinite(out.float()).all()
     assert out.float().abs().max() > 2.0 ** 16  # beyond fp16's range
     _check_benchmark_regime((out.float() * 2.0 ** -24).to(out.dtype), lse, kw)
+
+
+@requires_gpu
+@pytest.mark.parametrize("separate", [False, True])
+def test_split_partials_of_small_values(separate):
+    # the mirror case: cache values 2^-24 times the usual size (q scaled up by as
+    # much) make every partial row lie below fp16's normal range (2^-14) unless
+    # scaled up; golden is exactly 2^-24 times golden on the unscaled inputs, so the
+    # result times 2^24 is checked against golden on those, with every item split,
+    # for the merge inside the attention kernel and for the merge kernel
+    _say(f"split partials of small values (separate merge kernel: {separate})")
+    kw = _reduced_workload("mla_decode_b64_h128_k2048", 2, seed=17)
+    small = dict(kw)
+    for key in ("ori_kv", "cmp_kv"):
+        small[key] = kw[key] * 2.0 ** -24
+    small["q"] = kw["q"] * 2.0 ** 24
+    prep = api.prepare(**_dev(small), core_num=256, _separate_merge=separate)
+    assert prep.args.num_fd > 0
+    api.launch(prep)
+    torch.cuda.synchronize()
+    out = prep.out.reshape(kw["q"].shape[:-1] + (512,))
+    lse = prep.lse.reshape(kw["q"].shape[:-1])
+    assert torch.isfinite(out.float()).all()
+    assert 0 < out.float().abs().max() < 2.0 ** -14  # below fp16's normal range
+    _check_benchmark_regime((out.float() * 2.0 ** 24).to(out.dtype), lse, kw)

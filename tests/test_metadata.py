@@ -44,7 +44,7 @@ def _kwargs(cfg, **over):
 
 def _items(act_q, act_kv, n1, win_left, scen, ratio, topk, s2b):
     """Independent restatement of the item list: [(b, m, nblk)]."""
-    mb = M.m_base_for(n1)
+    mb = M.m_base_for(n1, batch=len(act_q))
     hb = (n1 + mb - 1) // mb
     items = []
     for b, (aq, ak) in enumerate(zip(act_q, act_kv)):
@@ -76,6 +76,7 @@ def _check_schedule(md, act_q, act_kv, n1, win_left, scen, ratio, topk, ncores):
         prev = tuple(r[4:7])
     assert prev == (len(act_q), 0, 0)
     # exact-once block coverage and partial-slot bookkeeping
+    assert cfg["m_base"] == M.m_base_for(n1, batch=len(act_q))
     items = _items(act_q, act_kv, n1, win_left, scen, ratio, topk, cfg["s2_base"])
     import bisect
     keys = [(b, m) for (b, m, _) in items]
@@ -114,7 +115,7 @@ def _check_schedule(md, act_q, act_kv, n1, win_left, scen, ratio, topk, ncores):
     # FD rows: one group per split item, contiguous slots in core order
     fd_used = [r for r in fd if r[0] == 1]
     assert len(fd_used) == cfg["num_fd"]
-    mb = min(n1, M.m_base_for(n1))
+    mb = min(n1, cfg["m_base"])
     by_item = {}
     for r in fd_used:
         by_item.setdefault((r[1], r[2]), []).append(r)

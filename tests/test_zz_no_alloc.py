@@ -5,8 +5,10 @@ in the library's fixed per-device scratch array instead of the caller's
 workspace. Checked through the C-ABI: bitwise-equal outputs to
 ``sas_attention_launch`` on two calls in a row (the second on a smaller
 input, so the scratch array holds the first call's partials when it starts),
-for host-built schedules with split items and for a device-built schedule;
-and a schedule whose partials do not fit is refused before any launch.
+for host-built schedules with split items and for a device-built schedule,
+with the merge kernel and with the merge inside the attention kernel (whose
+arrival counters sit in the scratch array too); and a schedule whose partials
+do not fit is refused before any launch.
 """
 
 import ctypes
@@ -55,6 +57,25 @@ def test_noalloc_matches_launch_two_calls(name, batches, extra):
         prep = api.prepare(**kw, **extra)
         assert prep.args.num_fd != 0, "the case must exercise the split-KV workspace"
         o_ref, l_ref = _launch("sas_attention_launch", prep)
+        o, l = _launch("sas_attention_launch_noalloc", prep)
+        assert torch.isfinite(o_ref.float()).all()
+        assert torch.equal(o, o_ref) and torch.equal(l, l_ref)
+
+
+@requires_gpu
+def test_noalloc_merge_in_kernel_two_calls():
+    # a non-null merge_sync selects the merge inside the attention kernel; the
+    # allocation-free entry point keeps its arrival counters in the scratch array
+    # (the caller's pointer is not used), zero at load and after every call
+    for batch in (8, 2):
+        _say(f"merge in kernel, batch={batch}")
+        kw = gen.build_workload("mla_decode_b64_h128_k2048", device="cuda", seed=60 + batch,
+                                batch=batch)
+        prep = api.prepare(**kw, core_num=256, _m_base=128 if batch == 8 else 64)
+        assert prep.args.num_fd != 0
+        prep.args.merge_sync = None
+        o_ref, l_ref = _launch("sas_attention_launch", prep)  # merge kernel
+        prep.args.merge_sync = 8  # any non-null 8-byte-aligned value
         o, l = _launch("sas_attention_launch_noalloc", prep)
         assert torch.isfinite(o_ref.float()).all()
         assert torch.equal(o, o_ref) and torch.equal(l, l_ref)
