@@ -33,8 +33,8 @@ from typing import Optional, Tuple, Union
 import torch
 
 from . import _lib
-from .metadata import (AIC_CORE_NUM, DEFAULT_CORE_NUM, DEFAULT_S2_BASE,  # noqa: F401
-                       SAS_META_SIZE,
+from .metadata import (AIC_CORE_NUM, CFG_OFFSET, DEFAULT_CORE_NUM,  # noqa: F401
+                       DEFAULT_S2_BASE, FD_METADATA_SIZE, FD_OFFSET, SAS_META_SIZE,
                        build_metadata, build_metadata_device, config_row, m_base_for,
                        m_base_valid)
 
@@ -77,13 +77,32 @@ class Prepared:
     merge_in_kernel: bool = True  # split items merged by their last piece (SasAttnArgs.merge_sync)
 
 
+# Split items are merged inside the attention kernel (by the piece that finishes
+# last) when no item has more than this many pieces; with more, the merge kernel
+# spreads the merging over all compute units and is faster (measured on MI355X:
+# items of 2 pieces merge in ~2 us less inside the kernel; items of 8 pieces take
+# ~3 us longer there).
+MERGE_IN_KERNEL_MAX_PIECES = 2
+
+
+def _max_pieces(md: torch.Tensor) -> int:
+    """Largest piece count of a split item in a host schedule (0: nothing split)."""
+    cfg = md[CFG_OFFSET:CFG_OFFSET + 8].tolist()
+    nfd = int(cfg[3])
+    if nfd <= 0:
+        return 0
+    fd = md[FD_OFFSET:FD_OFFSET + nfd * FD_METADATA_SIZE].view(nfd, FD_METADATA_SIZE)
+    return int(fd[:, 4].max().item())
+
+
 @functools.lru_cache(maxsize=64)
 def _cached_schedule(act_q: tuple, act_kv: tuple, num_heads: int, ori_win_left: int,
                      scenario: int, cmp_ratio: int, topk: int, core_num: int,
-                     fp8: bool, m_base: Optional[int] = None) -> torch.Tensor:
-    return build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads,
-                          ori_win_left=ori_win_left, scenario=scenario, cmp_ratio=cmp_ratio,
-                          cmp_topk=topk, core_num=core_num, fp8=fp8, m_base=m_base)
+                     fp8: bool, m_base: Optional[int] = None) -> Tuple[torch.Tensor, int]:
+    md = build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads,
+                        ori_win_left=ori_win_left, scenario=scenario, cmp_ratio=cmp_ratio,
+                        cmp_topk=topk, core_num=core_num, fp8=fp8, m_base=m_base)
+    return md, _max_pieces(md)
 
 
 # Schedules built by the on-device scheduler for calls without ``metadata``: one
@@ -160,7 +179,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             schedule: Optional[str] = None,
             fp8_qk: bool = False,
             _stream_schedule: bool = False,
-            _pipelined: bool = False, _separate_merge: bool = False,
+            _pipelined: bool = False, _separate_merge: Optional[bool] = None,
             _m_base: Optional[int] = None) -> Prepared:
     """Validate and stage one call (host work of api.py:186-384) without launching.
 
@@ -174,8 +193,9 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     prepared call schedules into a buffer of its own. ``_pipelined`` (tests): native
     rows run through the kernel fp8 rows use (``SAS_PHASE_PIPELINED``, items of at
     most 64 heads), for bitwise comparisons with the fp8 path. ``_separate_merge``
-    (tests, timing): split items are merged by the merge kernel after the attention
-    kernel instead of inside it. ``_m_base`` (tests, timing): heads per item instead
+    (tests, timing): True merges split items by the merge kernel after the attention
+    kernel, False inside it; None (default) inside it when no item has more than
+    ``MERGE_IN_KERNEL_MAX_PIECES`` pieces. ``_m_base`` (tests, timing): heads per item instead
     of ``m_base_for``'s choice (a call with its own ``metadata`` uses the metadata's).
     """
     del seqused_q  # API-parity placeholder (api.py:186)
@@ -335,15 +355,23 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
         cap = int(core_num) if metadata is None else AIC_CORE_NUM
         cfg = dict(num_fa=cap, num_fd=_lib.SCHED_DEVICE, num_partial_slots=2 * cap,
                    s2_base=DEFAULT_S2_BASE, m_base=m_base)
+        # pieces per item are not known on the host: expect at most two when the
+        # items are at least half as many as the workgroups
+        items = total * ((n1 + cfg["m_base"] - 1) // cfg["m_base"])
+        few_pieces = int(core_num) <= MERGE_IN_KERNEL_MAX_PIECES * items
     elif metadata is None:
         kv_host = tuple(int(x) for x in seqused_kv.to(torch.int32).cpu().tolist())
-        md = _cached_schedule(tuple(act_q), kv_host, int(n1), int(ori_win_left), scenario,
-                              cmp_ratio_eff, int(k), int(core_num), item64, m_base)
+        md, max_pieces = _cached_schedule(tuple(act_q), kv_host, int(n1), int(ori_win_left),
+                                          scenario, cmp_ratio_eff, int(k), int(core_num),
+                                          item64, m_base)
         cfg = config_row(md)
         metadata_dev = md.to(dev, non_blocking=True)
+        few_pieces = max_pieces <= MERGE_IN_KERNEL_MAX_PIECES
     else:
         metadata_dev = metadata.to(dev).to(torch.int32).reshape(SAS_META_SIZE).contiguous()
         cfg = config_row(metadata)  # host read of the schedule summary row
+        few_pieces = _max_pieces(metadata.to("cpu", torch.int32).reshape(-1)) <= \
+            MERGE_IN_KERNEL_MAX_PIECES
         assert cfg["num_heads"] == n1 and m_base_valid(n1, item64, cfg["m_base"]), (
             "metadata was built for a different head count or cache row format "
             "(fp8 cache rows: sparse_attn_sharedkv_metadata(..., kv_cache_dtype='fp8_ds_mla'))")
@@ -399,7 +427,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                     bsnd_shape=None if layout_q == "TND" else (nb, total // max(nb, 1), n1, dv),
                     device=dev, phase_bits=(_lib.SAS_PHASE_FP8_QK if fp8_qk else 0) |
                     (_lib.SAS_PHASE_PIPELINED if _pipelined else 0),
-                    merge_in_kernel=not _separate_merge)
+                    merge_in_kernel=few_pieces if _separate_merge is None
+                    else not _separate_merge)
 
 
 def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: int = 0) -> None:

@@ -108,7 +108,8 @@ def test_merge_in_kernel_back_to_back_schedules():
                                 batch=batch)
         _, o_sep, l_sep = _call(kw, True, core_num=cores, _m_base=mb)
         expect.append((kw, cores, mb, o_sep, l_sep))
-    preps = [api.prepare(**kw, core_num=cores, _m_base=mb) for kw, cores, mb, _, _ in expect]
+    preps = [api.prepare(**kw, core_num=cores, _m_base=mb, _separate_merge=False)
+             for kw, cores, mb, _, _ in expect]
     for p in preps:
         api.launch(p)  # no synchronisation between the calls
     torch.cuda.synchronize()
@@ -126,3 +127,18 @@ def test_merge_in_kernel_device_schedule():
     _, o, l = _call(kw, False, schedule="device")
     assert torch.equal(o, o_sep) and torch.equal(l, l_sep)
     _sync_words_zero()
+
+
+@requires_gpu
+@pytest.mark.parametrize("name,batch,cores,fused", [
+    ("mla_decode_b64_h128_k2048", 64, 256, True),      # 64-head items in 2 pieces
+    ("swa_topk_decode_b32_h64_k512", 32, 256, False),  # items of 8 pieces
+    ("mla_decode_b64_h128_k2048", 8, 256, False),
+])
+def test_merge_placement_default(name, batch, cores, fused):
+    # by default items of at most two pieces are merged in the attention kernel,
+    # items of more pieces by the merge kernel, on host- and device-built schedules
+    kw = gen.build_workload(name, device="cuda", seed=5, batch=batch)
+    for sched in ("host", "device"):
+        prep = api.prepare(**kw, core_num=cores, schedule=sched)
+        assert prep.merge_in_kernel == fused, (sched, prep.merge_in_kernel)
