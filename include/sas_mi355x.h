@@ -177,8 +177,10 @@ typedef struct SasAttnArgs {
    * two kernels agree to within rounding, not bit for bit.
    * SAS_PHASE_FP8_QK (bit 3, fp8 rows only) forms Q·Kᵀ on fp8 MFMA
    * (v_mfma_f32_16x16x128_f8f6f4): each head's 512 latent query dims are quantized
-   * to e4m3 with one fp32 scale (amax / 448, q / scale rounded to nearest even), the
-   * cache rows' e4m3 dims are used as stored, and each row's 128-dim block scales and
+   * to e4m3 with one fp32 scale: inv = 448 / amax (an IEEE fp32 division), codes =
+   * RNE_e4m3(clamp(q * inv, -448, 448)) (the product in fp32), scale sq = amax / 448
+   * (inv = sq = 1 for an all-zero head);
+   * the cache rows' e4m3 dims are used as stored, and each row's 128-dim block scales and
    * the head's scale are applied to the four block dot products in fp32; the rope
    * dims stay bf16. P·V stays on the dequantized bf16 rows. No reference counterpart
    * (kernel.py:2036-2352 forms Q·Kᵀ in bf16): it adds the query's quantization error,

@@ -10,7 +10,9 @@
   gives bitwise the outputs of the host-scheduled launch.
 * The whole call -- scheduler, attention, merge -- captured in one HIP graph
   and replayed with new sequence lengths written in place, every replay
-  bitwise equal to the eager host-scheduled call.
+  bitwise equal to the eager host-scheduled call; two calls captured into two
+  graphs and replayed in alternation likewise (each capture owns its schedule
+  and arrival-counter buffers).
 * A schedule the kernels cannot use (wrong head count, a negative length)
   turns every output into NaN instead of leaving stale memory.
 """
@@ -168,6 +170,44 @@ def test_whole_call_in_one_graph_with_new_lengths_each_replay():
         got_o, got_l = out.clone(), lse.clone()
         ref_o, ref_l = _run(sparse_flash_mla, dict(kw, seqused_kv=lens.clone()), schedule="host")
         assert torch.equal(got_o, ref_o) and torch.equal(got_l, ref_l), f"replay {r}"
+        assert torch.isfinite(got_o.float()).all()
+
+
+@requires_gpu
+def test_two_graphs_replayed_alternately():
+    # two calls captured into two graphs (the same capture stream), each with its
+    # own schedule and arrival-counter buffers, replayed in alternation with new
+    # lengths; every replay bitwise the eager host-scheduled call
+    _say("two captured graphs replayed alternately")
+    kws = [gen.build_workload("mla_decode_b64_h128_k2048", device="cuda", seed=11, batch=64),
+           gen.build_workload("swa_topk_decode_b32_h64_k512", device="cuda", seed=12, batch=5)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up off the capture
+        for kw in kws:
+            sparse_flash_mla(**kw, schedule="device", return_softmax_lse=True)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graphs, outs = [], []
+    for kw in kws:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(sparse_flash_mla(**kw, schedule="device", return_softmax_lse=True))
+        graphs.append(g)
+    base = [kw["seqused_kv"].clone() for kw in kws]
+    rng = np.random.default_rng(3)
+    for r in range(6):
+        i = r % 2
+        kw = kws[i]
+        lens = base[i] if r < 2 else torch.tensor(
+            rng.integers(2100, int(base[i].max()) + 1, size=base[i].numel()),
+            dtype=torch.int32, device="cuda")
+        kw["seqused_kv"].copy_(lens)
+        graphs[i].replay()
+        torch.cuda.synchronize()
+        got_o, got_l = outs[i][0].clone(), outs[i][1].clone()
+        ref_o, ref_l = _run(sparse_flash_mla, dict(kw, seqused_kv=lens.clone()), schedule="host")
+        assert torch.equal(got_o, ref_o) and torch.equal(got_l, ref_l), f"replay {r} (graph {i})"
         assert torch.isfinite(got_o.float()).all()
 
 

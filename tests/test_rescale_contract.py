@@ -194,3 +194,28 @@ def test_split_with_fp16_partials_matches_fp32_partials():
     row = o32.float().abs().amax(dim=1, keepdim=True)
     assert (d <= 2.0 ** -10 * row + torch.finfo(torch.bfloat16).eps * o32.float().abs()).all()
     assert (d > 0).float().mean() < 0.05
+
+
+def test_rescale_study_reproduces_the_sweep_figures():
+    # ``oracle.rescale_study`` (the 300-configuration study behind the contract)
+    # on the three configurations that set its worst figures: 16 is the lowest
+    # agreement for golden at 64-row tiles, the kernel's order and fp16 split
+    # partials (the one configuration under 99.25 % with fp16 partials); 138 is the
+    # one where the kernel's order (and fp16 split partials) put one element beyond
+    # 2e-2; 48 is one where bf16 partials would put 8 elements beyond 2e-2 and fp16
+    # partials none (the worst has 19) -- why the split pieces are stored in fp16.
+    from oracle import rescale_study as R
+
+    rows = {i: R.run_case(i) for i in (16, 138, 48)}
+    r16, r138, r48 = rows[16], rows[138], rows[48]
+    assert 99.25 <= r16["golden64"]["pct_ref"] < 99.5
+    assert r16["golden64"]["beyond_2e2"] == 0
+    assert r16["t64_tau0"]["pct_ref"] == pytest.approx(99.296, abs=1e-3)
+    assert 99.2 <= r16["t64_split2_f16"]["pct_ref"] < 99.25
+    assert r138["golden64"]["beyond_2e2"] == 0
+    assert r138["t64_tau0"]["beyond_2e2"] == 1 and r138["t64_split2_f16"]["beyond_2e2"] == 1
+    assert r48["t64_split2_bf16"]["beyond_2e2"] == 8
+    assert r48["t64_split2_f16"]["beyond_2e2"] == 0
+    s = R.summarize(list(rows.values()))
+    assert s["t64_tau0"]["min_pct"] >= 99.25 and s["t64_tau0"]["max_beyond_2e2"] <= 1
+    assert s["t64_split2_f16"]["max_ratio_exact"] <= 1.25
