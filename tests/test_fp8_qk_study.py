@@ -57,11 +57,17 @@ def test_fp8_scores_exact_on_exactly_representable_operands():
     k = st.dequant_bf16(raw).astype(np.float64)
     scale = 1 / math.sqrt(576)
     expect = ((q.astype(np.float64) @ k.T) * scale).astype(np.float32)
-    assert np.array_equal(scores_fp8(q, raw, scale), expect)
+    assert np.array_equal(scores_fp8(q, raw, scale, dot="exact"), expect)
     # block 1's scales replaced by 1.0: visible in the scores
     raw2 = raw.copy()
     raw2[:, 516:520] = np.frombuffer(np.full(n, 1.0, "<f4").tobytes(), np.uint8).reshape(n, 4)
-    assert not np.array_equal(scores_fp8(q, raw2, scale), expect)
+    assert not np.array_equal(scores_fp8(q, raw2, scale, dot="exact"), expect)
+    # the MFMA form truncates each run of 8 products below its largest: never more
+    # than the run bound away from the exact scores, and not equal to them here
+    # (the codes span the whole e4m3 range)
+    mf = scores_fp8(q, raw, scale).astype(np.float64)
+    assert not np.array_equal(mf, expect)
+    assert np.allclose(mf, expect, rtol=0, atol=np.abs(expect).max() * 2.0 ** -6)
 
 
 def test_fp8_scores_equal_the_product_of_the_dequantized_operands():
@@ -79,8 +85,11 @@ def test_fp8_scores_equal_the_product_of_the_dequantized_operands():
     k_deq = np.concatenate([(k8 * sk[:, :, None]).reshape(-1, 512), rope], axis=1)
     scale = 1 / math.sqrt(576)
     expect = (q_deq @ k_deq.T) * scale
-    got = scores_fp8(q, raw, scale).astype(np.float64)
+    got = scores_fp8(q, raw, scale, dot="exact").astype(np.float64)
     assert np.allclose(got, expect, rtol=1e-5, atol=1e-6)
+    # on quantized N(0,1)-like data the MFMA form is within 2e-3 relative of that
+    got = scores_fp8(q, raw, scale).astype(np.float64)
+    assert np.allclose(got, expect, rtol=2e-3, atol=2e-3 * np.abs(expect).max())
 
 
 def test_benchmark_data_within_the_bound_reference_data_not():
