@@ -269,7 +269,9 @@ def main():
     attn_ms = per_launch(1)
     # split items are merged by the merge kernel, or inside the attention kernel
     # (native rows): then the attention launch includes the merge
-    merge_in_attn = preps[0].merge_in_kernel and not sets[0].get("kv_cache_dtype")
+    # (the 128-head kernel on either row format, the native-row kernel)
+    merge_in_attn = preps[0].merge_in_kernel and (
+        preps[0].args.m_base == 128 or not sets[0].get("kv_cache_dtype"))
     has_merge = preps[0].args.num_fd > 0 and not merge_in_attn
     merge_ms = per_launch(2) if has_merge else [0.0] * k  # no merge kernel
     attn_avg = sum(attn_ms) / k
@@ -277,10 +279,10 @@ def main():
     srt = attn_ms
 
     achieved = nbytes / (attn_avg * 1e-3) / 1e9
-    # fp8 rows run on the pipelined kernel; native rows on the 128-head kernel when
-    # an item holds 128 heads, else on the one-wave-per-SIMD kernel
-    kernel = ("sas::attn3_kernel" if sets[0].get("kv_cache_dtype")
-              else "sas::wide_kernel" if preps[0].args.m_base == 128 else "sas::attn2_kernel")
+    # items of 128 heads run on the 128-head kernel (either row format); smaller
+    # items on the pipelined kernel for fp8 rows, else the one-wave-per-SIMD kernel
+    kernel = ("sas::wide_kernel" if preps[0].args.m_base == 128
+              else "sas::attn3_kernel" if sets[0].get("kv_cache_dtype") else "sas::attn2_kernel")
     if w.get("prefill"):
         # prefill: consecutive query rows re-read each other's cache rows, which
         # stay on chip; the algorithmic HBM bytes are q, out and lse once plus the

@@ -98,10 +98,10 @@ def _max_pieces(md: torch.Tensor) -> int:
 @functools.lru_cache(maxsize=64)
 def _cached_schedule(act_q: tuple, act_kv: tuple, num_heads: int, ori_win_left: int,
                      scenario: int, cmp_ratio: int, topk: int, core_num: int,
-                     fp8: bool, m_base: Optional[int] = None) -> Tuple[torch.Tensor, int]:
+                     item64: bool, m_base: Optional[int] = None) -> Tuple[torch.Tensor, int]:
     md = build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads,
                         ori_win_left=ori_win_left, scenario=scenario, cmp_ratio=cmp_ratio,
-                        cmp_topk=topk, core_num=core_num, fp8=fp8, m_base=m_base)
+                        cmp_topk=topk, core_num=core_num, item64=item64, m_base=m_base)
     return md, _max_pieces(md)
 
 
@@ -269,8 +269,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
 
     kv_fmt = _kv_format(kv_cache_dtype, ori_kv)
     fp8_rows = kv_fmt == _lib.KV_FP8_DS_MLA
-    # items of at most 64 heads: fp8 rows and the pipelined kernel (m_base_for)
-    item64 = fp8_rows or _pipelined
+    # items of at most 64 heads: the fp8 Q·Kᵀ form and the pipelined kernel (m_base_for)
+    item64 = bool(fp8_qk) or _pipelined
     m_base = m_base_for(int(n1), item64, nb) if _m_base is None else int(_m_base)
     if not m_base_valid(int(n1), item64, m_base):
         raise ValueError(f"no kernel for items of {m_base} heads at {n1} heads")
@@ -343,7 +343,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
                 batch=nb, act_q=act_q_d, act_kv=seqused, num_heads=int(n1),
                 ori_win_left=int(ori_win_left), scenario=scenario, cmp_ratio=cmp_ratio_eff,
                 cmp_topk=int(k), core_num=int(core_num),
-                out=_schedule_buffer(dev) if _stream_schedule else None, fp8=item64,
+                out=_schedule_buffer(dev) if _stream_schedule else None, item64=item64,
                 m_base=m_base)
         else:
             metadata_dev = metadata.to(device=dev, dtype=i32).reshape(SAS_META_SIZE).contiguous()

@@ -2426,7 +2426,10 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     const int per_xcd = (a.num_fa + 7) / 8;
     // native rows: one wave per SIMD (attn2_kernel); fp8 rows: the pipelined
     // two-waves-per-SIMD kernel, whose second wave hides the dequantization
-    if constexpr (KVF == SAS_KV_FP8_DS_MLA) {
+    if constexpr (KVF == SAS_KV_FP8_DS_MLA && NHG == 4) {
+      // 128-head items of fp8 rows: the 128-head kernel, dequantizing a raw ring
+      hipLaunchKernelGGL((wide_kernel<DQK, 512, T, KVF>), dim3(8 * per_xcd), dim3(512), 0, st, a);
+    } else if constexpr (KVF == SAS_KV_FP8_DS_MLA) {
       if (a.phases & SAS_PHASE_FP8_QK)
         hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF, true>), dim3(8 * per_xcd),
                            dim3(256 * NHG), 0, st, a);
@@ -2451,10 +2454,11 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   const bool dev = a.num_fd == SAS_SCHED_DEVICE;
-  // the native-row kernels (128-head and one-wave-per-SIMD) merge split items
-  // themselves when given arrival counters
-  const bool merged_in_attn = KVF == SAS_KV_NATIVE && !(a.phases & SAS_PHASE_PIPELINED) &&
-                              a.merge_sync != nullptr && a.workspace != nullptr;
+  // the 128-head kernel and the native-row one-wave-per-SIMD kernel merge split
+  // items themselves when given arrival counters
+  const bool merged_in_attn =
+      (NHG == 4 || (KVF == SAS_KV_NATIVE && !(a.phases & SAS_PHASE_PIPELINED))) &&
+      a.merge_sync != nullptr && a.workspace != nullptr;
   if ((phases & 2) && (a.num_fd > 0 || dev) && !merged_in_attn) {
     const int groups = (a.m_base + MERGE_HPB - 1) / MERGE_HPB;  // head groups per task (upper bound)
     const int tasks = dev ? (a.num_fa < 256 ? a.num_fa : 256) : a.num_fd;  // columns; tasks strided
@@ -2482,8 +2486,9 @@ static hipError_t dispatch_heads(const SasAttnArgs& a, hipStream_t st) {
 // fp8 rows: head_dim 576, bf16 queries and outputs
 static hipError_t dispatch_fp8(const SasAttnArgs& a, hipStream_t st) {
   constexpr int F8 = SAS_KV_FP8_DS_MLA;
-  return a.m_base == 32 ? launch_attn<576, 1, __bf16, F8>(a, st)
-                        : launch_attn<576, 2, __bf16, F8>(a, st);
+  return a.m_base == 32   ? launch_attn<576, 1, __bf16, F8>(a, st)
+         : a.m_base == 64 ? launch_attn<576, 2, __bf16, F8>(a, st)
+                          : launch_attn<576, 4, __bf16, F8>(a, st);
 }
 
 }  // namespace sas
@@ -2511,15 +2516,16 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     set_error("sas_attention_launch: num_heads must be a multiple of 16 in [16, 128]");
     return SAS_E_UNSUPPORTED;
   }
-  // heads per item: 32 up to 32 heads, 64 up to 64 heads, above that 128 for native
-  // rows (one item holds the token's every head) and 64 for fp8 rows and for native
-  // rows run through the pipelined kernel (SAS_PHASE_PIPELINED)
-  const bool item64 = a->kv_format == SAS_KV_FP8_DS_MLA || (a->phases & SAS_PHASE_PIPELINED);
+  // heads per item: 32 up to 32 heads, 64 up to 64 heads, above that 128 (one item
+  // holds the token's every head: the 128-head kernel) or 64; 64 only for the fp8
+  // Q·Kᵀ form (SAS_PHASE_FP8_QK) and for native rows run through the pipelined
+  // kernel (SAS_PHASE_PIPELINED)
+  const bool item64 = (a->phases & SAS_PHASE_FP8_QK) || (a->phases & SAS_PHASE_PIPELINED);
   const int want_mb = a->num_heads <= 32 ? 32 : (a->num_heads <= 64 || item64) ? 64 : 128;
-  // native rows above 64 heads may also be scheduled in 64-head items (two per token)
+  // above 64 heads items may also hold 64 heads (two per token)
   if (a->m_base != want_mb && !(want_mb == 128 && a->m_base == 64)) {
     set_error("sas_attention_launch: m_base must be 32 for <= 32 heads, 64 for <= 64 heads "
-              "(or fp8 rows, or SAS_PHASE_PIPELINED), else 128 or 64");
+              "(or SAS_PHASE_FP8_QK, or SAS_PHASE_PIPELINED), else 128 or 64");
     return SAS_E_INVALID;
   }
   if (a->scenario < 1 || a->scenario > 3 || (a->scenario >= 2 && (!a->cmp_kv ||

@@ -89,18 +89,30 @@ __device__ inline int wide_rope1(int l) {
 }
 __device__ inline int wide_v(int l) { return wide_row_base(4 * (l >> 4) + ((l & 15) >> 2)) + 8 * (l & 3); }
 
-template <int DQK, int DV, typename T>
+template <int DQK, int DV, typename T, int KVF = SAS_KV_NATIVE>
 __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   constexpr int NW = 8;                  // waves per workgroup
   constexpr int MB = 128;                // heads per item (m-block)
   constexpr int NT = 64 * NW;            // threads
   constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
-  constexpr int ROWB = DQK * 2;          // bytes per cache row in HBM
+  // fp8 rows (SAS_KV_FP8_DS_MLA): tiles arrive by DMA as raw 656-byte rows in a
+  // ring of their own and are dequantized into the bf16 stage layout one tile
+  // ahead of their use (the same bf16 values the native path computes on)
+  constexpr bool FP8 = KVF == SAS_KV_FP8_DS_MLA;
+  constexpr int ROWB = FP8 ? SAS_FP8_ROW_BYTES : DQK * 2;  // bytes per cache row in HBM
   constexpr int NKS = DQK / 32;          // 16x16x32 k-steps over d_qk (18 or 16)
   constexpr int NKS_MAIN = 16;           // k-steps over the 512 main dims
   constexpr int NDV = DV / 16;           // 16-wide dv blocks (32)
-  constexpr int NSTG = 4;                // LDS ring depth
+  constexpr int NSTG = FP8 ? 2 : 4;      // bf16 ring depth (fp8: the tile in use, the one filled)
   constexpr int STAGE_BYTES = WMAIN + (ROPE ? WROPE : 0);
+  constexpr int RAW_CH = SAS_FP8_ROW_BYTES / 16;  // 16-byte chunks per fp8 row (41)
+  constexpr int LATENT_BYTES = 512;      // fp8 row: e4m3 dims 0..511, then 4 fp32 scales, rope
+  constexpr int RAW_DMA = 3;             // fp8: raw DMA instructions per wave and tile (24 x 1 KB)
+  constexpr int RAW_STAGE = RAW_DMA * NW * 1024;  // 32 rows x 656 B (1312 chunks), padded
+  constexpr int NRAW = FP8 ? 3 : 0;      // raw ring depth
+  constexpr int LDS_BYTES = NSTG * STAGE_BYTES + NRAW * RAW_STAGE;
+  static_assert(!FP8 || (DQK == 576 && __is_same(T, __bf16)), "fp8 rows: d_qk 576, bf16");
+  static_assert(TILE * RAW_CH <= RAW_DMA * NW * 64, "raw stage chunks");
   constexpr int RPW = TILE / NW;         // main-part DMA instructions per wave and tile (4)
   constexpr int NROPE = ROPE ? TILE / 8 : 0;  // rope DMA instructions per tile (waves w < 4)
   constexpr int RCH = 1024;              // positions resolved into LDS at a time
@@ -108,11 +120,11 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   static_assert(DQK == 512 || DQK == 576, "head_dim");
   static_assert(DV == 512, "head_dim_v");
   static_assert(NROPE <= NW, "rope DMA split");
-  static_assert(MB * (DV * 2 + 16) <= NSTG * STAGE_BYTES, "output staging");
+  static_assert(MB * (DV * 2 + 16) <= LDS_BYTES, "output staging");
   typedef MfmaOps<T> Ops;
   typedef typename Ops::vec8 vec8;
 
-  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[NSTG * STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char kv_lds[LDS_BYTES];
   __shared__ uint32_t rowid[RCH];
   __shared__ uint32_t tmask[RCH / TILE];
   __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
@@ -434,14 +446,54 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       // this wave's DMAs of all but the newest one / two tiles have landed
       auto wait_all_but = [&](auto n_tiles) {
         constexpr int N = decltype(n_tiles)::value;
-        if (has_rope) wait_vmcnt<N * (RPW + 1)>();
+        if constexpr (FP8) wait_vmcnt<N * RAW_DMA>();
+        else if (has_rope) wait_vmcnt<N * (RPW + 1)>();
         else wait_vmcnt<N * RPW>();
       };
-
       typedef const unsigned char SAS_LDS* lds_p;
       auto stage_of = [&](int tile) -> lds_p {
         return (lds_p)(kv_base + (uint32_t)((tile % NSTG) * STAGE_BYTES));
       };
+      // ---- fp8 rows: raw DMA and dequantization ----
+      // Raw tile t goes to raw stage t % 3: this wave's instruction i fills
+      // chunks 64 (w + 8 i) + lane of the stage, chunk c being 16-byte piece
+      // c % 41 of tile row c / 41 (chunks past the tile read the zero row).
+      auto raw_base = [&](int tile) -> uint32_t {
+        return kv_base + (uint32_t)(NSTG * STAGE_BYTES + (tile % 3) * RAW_STAGE);
+      };
+      auto raw_issue = [&](int tile, int i) {
+        const int c = 64 * (w + NW * i) + lane_id_here();
+        const char* src = (const char*)g_zero_row;
+        if (tile < ntile && c < TILE * RAW_CH) {
+          const int r = c / RAW_CH;
+          src = row_ptr(rowid[tile * TILE + r]) + 16 * (c - r * RAW_CH);
+        }
+        dma16_vaddr(src, raw_base(tile) + (uint32_t)((w + NW * i) * 1024));
+      };
+      // Raw tile t (landed and published by a barrier) into bf16 stage t % 2:
+      // thread x dequantizes dims 32 (x % 16) .. + 31 of tile row x / 16 as
+      // bf16(fp32(e4m3) * scale) and, for x % 16 < 8, copies rope chunk x % 16.
+      auto convert = [&](int tile) {
+        // (the thread's index recomputed here, so no offset stays live across the loop)
+        const int x = 64 * w + lane_id_here();
+        const int r = x >> 4, j = x & 15;
+        const lds_p raw = (lds_p)(raw_base(tile) + (uint32_t)(r * SAS_FP8_ROW_BYTES));
+        const uint32_t st = kv_base + (uint32_t)((tile % 2) * STAGE_BYTES);
+        typedef i16x8 SAS_LDS* lds8;
+        lds8 dst = (lds8)(st + (uint32_t)(wide_row_base(r) + 64 * j));
+        const float sc8 = *(const float SAS_LDS*)(raw + LATENT_BYTES + 4 * (j >> 2));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {  // one 16-byte half at a time
+          const i32x4 v = *(const i32x4 SAS_LDS*)(raw + 32 * j + 16 * h);
+          dst[2 * h] = fp8x8_dequant_bf16(make_uint2((uint32_t)v[0], (uint32_t)v[1]), sc8);
+          dst[2 * h + 1] = fp8x8_dequant_bf16(make_uint2((uint32_t)v[2], (uint32_t)v[3]), sc8);
+        }
+        if (j < 8) {
+          const i16x8 rp = *(const i16x8 SAS_LDS*)(raw + LATENT_BYTES + 16 + 16 * j);
+          *(lds8)(st + (uint32_t)(WMAIN + 16 * wide_rope_slot(wide_perm(r), j))) = rp;
+        }
+      };
+
       auto mma16 = [&](i16x8 x, i16x8 y, f32x4 c) -> f32x4 {
         return __is_same(T, __bf16)
                    ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(vec8, x),
@@ -536,14 +588,14 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       // ---- rescale (skipped when no head of the wave moved its maximum), then
       // P·V with Vᵀ operands VPF MFMAs ahead and the DMA instructions of `dd`
       // (the tile three ahead) between the MFMAs ----
-      auto pv_tile = [&](lds_p sb, i16x8 pk, float alpha, const DmaAddrs& dd) {
+      auto pv_tile = [&](lds_p sb, i16x8 pk, float alpha, const DmaAddrs& dd, int t) {
         if (__ballot(alpha != 1.0f) != 0) {
 #pragma unroll
           for (int d = 0; d < NDV; ++d)
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[d][j] *= alpha;
         }
-        constexpr int VPF = SAS_WVPF;
+        constexpr int VPF = FP8 ? 2 : SAS_WVPF;  // (fp8: two, making room for the dequantization)
         typedef i16x4 SAS_LDS* lds4;
         const lds_p vbase = sb + wide_v(lane_id_here());
         auto vop = [&](int d) -> i16x8 {
@@ -560,16 +612,32 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
           const i16x8 op = vb[d % VPF];
           if (d + VPF < NDV) vb[d % VPF] = vop(d + VPF);
           acc[d] = mma16(op, pk, acc[d]);
+          if constexpr (FP8) {
+            // the raw DMAs of tile t + 3 (into the raw stage tile t held), and
+            // tile t + 1's dequantization into the bf16 stage tile t - 1 held
 #pragma unroll
-          for (int j = 0; j < DMA_MAX; ++j)
-            if (d == 3 + 6 * j) dma_one(dd, j);
+            for (int j = 0; j < RAW_DMA; ++j)
+              if (d == 3 + 6 * j) raw_issue(t + 3, j);
+            if (d == 20 && t + 1 < ntile) convert(t + 1);
+          } else {
+#pragma unroll
+            for (int j = 0; j < DMA_MAX; ++j)
+              if (d == 3 + 6 * j) dma_one(dd, j);
+          }
         }
       };
 
       // ---- prologue: tiles 0, 1, 2 in flight, then the query fragment ----
-      issue(next_addrs(0));
-      issue(next_addrs(1));
-      issue(next_addrs(2));
+      if constexpr (FP8) {
+#pragma unroll
+        for (int tt = 0; tt < 3; ++tt)
+#pragma unroll
+          for (int j = 0; j < RAW_DMA; ++j) raw_issue(tt, j);
+      } else {
+        issue(next_addrs(0));
+        issue(next_addrs(1));
+        issue(next_addrs(2));
+      }
       if (c0 == p_lo) {
         load_q();
         // (the compiler's wait for the query loads goes here, before the tile loop;
@@ -577,21 +645,35 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) asm volatile("" ::"v"(qf[ks]));
       }
+      if constexpr (FP8) {
+        wait_all_but(std::integral_constant<int, 2>{});  // this wave's raw DMAs of tile 0
+        __syncthreads();                                  // every wave's
+        convert(0);
+      }
 
       // ---- tile loop: before barrier t every wave has waited for its DMAs of tile
       // t (tiles t + 1 and t + 2 may be in flight); after it every wave is done with
       // tile t - 1, whose stage takes the DMAs of tile t + 3, issued between this
-      // tile's P·V MFMAs: three tiles in flight under the compute of one ----
+      // tile's P·V MFMAs: three tiles in flight under the compute of one. fp8 rows:
+      // before barrier t every wave has waited for its raw DMAs of tile t + 1
+      // (t + 2 may be in flight), which tile t dequantizes into the bf16 stage of
+      // t - 1 while tile t (dequantized during t - 1) is computed, and the raw DMAs
+      // of t + 3 go to the raw stage of t ----
       for (int t = 0; t < ntile; ++t) {
         const lds_p sb = stage_of(t);
-        wait_all_but(std::integral_constant<int, 2>{});  // this wave's share of tile t
-        __syncthreads();                                  // barrier t
+        if constexpr (FP8) wait_all_but(std::integral_constant<int, 1>{});
+        else wait_all_but(std::integral_constant<int, 2>{});  // this wave's share of tile t
+        __syncthreads();                                       // barrier t
         f32x4 s0, s1;
         qk_tile(sb, s0, s1);
         float alpha;
         const i16x8 pk = softmax_tile(t, s0, s1, alpha);
-        const DmaAddrs dd = next_addrs(t + 3);
-        pv_tile(sb, pk, alpha, dd);
+        if constexpr (FP8) {
+          pv_tile(sb, pk, alpha, DmaAddrs{}, t);
+        } else {
+          const DmaAddrs dd = next_addrs(t + 3);
+          pv_tile(sb, pk, alpha, dd, t);
+        }
       }
       wait_vmcnt<0>();  // the last (zero-row) DMAs have landed ...
       __syncthreads();  // ... for every wave, before LDS is reused

@@ -53,27 +53,28 @@ DEFAULT_FD_HEAD_CHUNK = 64    # heads per merge task (a whole 64-head item)
 WIDE_ITEM_MIN_BATCH = 128
 
 
-def m_base_for(num_heads: int, fp8: bool = False, batch: Optional[int] = None) -> int:
+def m_base_for(num_heads: int, item64: bool = False, batch: Optional[int] = None) -> int:
     """Heads per schedulable item (the reference's mBaseSize, metadata.py:388).
 
     32 up to 32 heads and 64 up to 64 heads, as the reference. Above 64 heads an
-    item holds all of a token's heads (128) for native bf16 / fp16 rows when the
-    call has at least ``WIDE_ITEM_MIN_BATCH`` sequences (``batch``; a kernel then
-    serves every head of the token from one gathered tile), else 64; fp8 cache rows
-    (``fp8=True``) keep 64. The rule reads only values both schedulers and every
-    entry point know alike (head count, row format, sequence count)."""
+    item holds all of a token's heads (128) when the call has at least
+    ``WIDE_ITEM_MIN_BATCH`` sequences (``batch``; the 128-head kernel then serves
+    every head of the token from one gathered tile, native or fp8 rows), else 64;
+    ``item64`` (the fp8 Q·Kᵀ form, the pipelined kernel on native rows) keeps 64.
+    The rule reads only values both schedulers and every entry point know alike
+    (head count, kernel form, sequence count)."""
     if num_heads <= 32:
         return 32
-    if num_heads <= 64 or fp8 or batch is None or batch < WIDE_ITEM_MIN_BATCH:
+    if num_heads <= 64 or item64 or batch is None or batch < WIDE_ITEM_MIN_BATCH:
         return 64
     return 128
 
 
-def m_base_valid(num_heads: int, fp8: bool, m_base: int) -> bool:
-    """Item sizes the kernels accept for a head count and row format."""
+def m_base_valid(num_heads: int, item64: bool, m_base: int) -> bool:
+    """Item sizes the kernels accept for a head count and kernel form."""
     if num_heads <= 32:
         return m_base == 32
-    if num_heads <= 64 or fp8:
+    if num_heads <= 64 or item64:
         return m_base == 64
     return m_base in (64, 128)
 
@@ -127,15 +128,16 @@ def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: in
                    ori_win_left: int, scenario: int, cmp_ratio: int, cmp_topk: int,
                    core_num: int = DEFAULT_CORE_NUM, s2_base: int = DEFAULT_S2_BASE,
                    min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
-                   fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK, fp8: bool = False,
+                   fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK, item64: bool = False,
                    m_base: Optional[int] = None) -> torch.Tensor:
     """Run the C++ scheduler; returns an int32 CPU tensor of ``SAS_META_SIZE`` words.
-    ``fp8``: the schedule is for fp8 cache rows (64-head items, ``m_base_for``);
-    ``m_base``: the item size (default ``m_base_for``)."""
+    ``item64``: the schedule is for a kernel form of 64-head items at most (the fp8
+    Q·Kᵀ form, the pipelined kernel; ``m_base_for``); ``m_base``: the item size
+    (default ``m_base_for``)."""
     lib = _lib.load()
     b = len(act_q)
     if m_base is None:
-        m_base = m_base_for(int(num_heads), fp8, b)
+        m_base = m_base_for(int(num_heads), item64, b)
     out = torch.zeros(SAS_META_SIZE, dtype=torch.int32)
     aq = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_q])
     ak = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_kv])
@@ -194,7 +196,7 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
                           min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
                           fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK,
                           stream: Optional[torch.cuda.Stream] = None,
-                          out: Optional[torch.Tensor] = None, fp8: bool = False,
+                          out: Optional[torch.Tensor] = None, item64: bool = False,
                           m_base: Optional[int] = None) -> torch.Tensor:
     """Run the on-device scheduler (``sas_metadata_build_device``) on the current stream.
 
@@ -227,7 +229,7 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
         raise ValueError(f"out must be a contiguous int32 [{SAS_META_SIZE}] tensor on {dev}")
     st = stream if stream is not None else torch.cuda.current_stream(dev)
     if m_base is None:
-        m_base = m_base_for(int(num_heads), fp8, int(batch))
+        m_base = m_base_for(int(num_heads), item64, int(batch))
     rc = lib.sas_metadata_build_device(
         ctypes.c_void_p(out.data_ptr()), int(batch),
         ctypes.c_void_p(act_q.data_ptr() if act_q is not None else 0), int(uniform_q),
@@ -277,6 +279,7 @@ def sparse_attn_sharedkv_metadata(
     aiv_core_num: int = 2 * DEFAULT_CORE_NUM,
     device: Optional[str] = None,
     kv_cache_dtype: Optional[str] = None,
+    fp8_qk: bool = False,
 ) -> torch.Tensor:
     """Schedule for one ``sparse_attn_sharedkv`` call: int32 ``[SAS_META_SIZE]``.
 
@@ -290,9 +293,10 @@ def sparse_attn_sharedkv_metadata(
     schedule is built there by the on-device scheduler from the lengths moved to
     (or already on) that GPU, without reading them back; the words are the ones
     the host scheduler produces. ``kv_cache_dtype`` (no reference counterpart):
-    ``"fp8_ds_mla"`` builds the schedule for calls on fp8 cache rows, whose items
-    hold at most 64 heads. Items hold 32, 64 or 128 heads (``m_base_for``: 128 only
-    for native rows above 64 heads with at least ``WIDE_ITEM_MIN_BATCH`` sequences).
+    ``"fp8_ds_mla"`` for calls on fp8 cache rows, and ``fp8_qk`` (no reference
+    counterpart) for calls of the fp8 Q·Kᵀ form, whose items hold at most 64 heads.
+    Items hold 32, 64 or 128 heads (``m_base_for``: 128 only above 64 heads with at
+    least ``WIDE_ITEM_MIN_BATCH`` sequences).
     """
     del cu_seqlens_cmp_kv, head_dim, ori_topk, aiv_core_num
     if num_heads_kv != 1:
@@ -310,7 +314,9 @@ def sparse_attn_sharedkv_metadata(
     else:
         scenario = 1
     core_num = min(int(aic_core_num), AIC_CORE_NUM)
-    fp8 = _is_fp8(kv_cache_dtype)
+    if fp8_qk and not _is_fp8(kv_cache_dtype):
+        raise ValueError("fp8_qk needs kv_cache_dtype='fp8_ds_mla'")
+    item64 = bool(fp8_qk)
     if device is not None and torch.device(device).type == "cuda":
         # scheduled on that GPU from device-resident lengths: nothing is read back
         batch, act_q, uniform_q, act_kv = device_lengths(
@@ -321,7 +327,7 @@ def sparse_attn_sharedkv_metadata(
                                      act_kv=act_kv, num_heads=num_heads_q,
                                      ori_win_left=ori_win_left, scenario=scenario,
                                      cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
-                                     core_num=core_num, fp8=fp8)
+                                     core_num=core_num, item64=item64)
     act_q, act_kv = resolve_lengths(layout_q=layout_q, layout_kv=layout_kv,
                                     cu_seqlens_q=cu_seqlens_q,
                                     cu_seqlens_ori_kv=cu_seqlens_ori_kv, seqused_q=seqused_q,
@@ -330,5 +336,5 @@ def sparse_attn_sharedkv_metadata(
     md = build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads_q,
                         ori_win_left=ori_win_left, scenario=scenario,
                         cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
-                        core_num=core_num, fp8=fp8)
+                        core_num=core_num, item64=item64)
     return md.to(device) if device is not None else md

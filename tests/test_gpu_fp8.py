@@ -187,6 +187,33 @@ def test_fp8_equals_bf16_path_on_dequantized_cache(cores):
     _check(out_d, lse_d, _dequant_kw(kw))
 
 
+def _run_items(kw, m_base, **extra):
+    """The call with items of ``m_base`` heads (128: the 128-head kernel)."""
+    kw = {k: v for k, v in _dev(kw).items() if k != "topk_cmp"}
+    prep = api.prepare(**kw, **extra, _m_base=m_base)
+    assert prep.args.m_base == m_base
+    api.launch(prep)
+    torch.cuda.synchronize()
+    return prep.out.clone(), prep.lse.clone()
+
+
+@requires_gpu
+@pytest.mark.parametrize("cores", [256, 64, 7])
+def test_fp8_128_head_items_equal_bf16_on_dequantized_cache(cores):
+    # 128-head items: the 128-head kernel dequantizes each raw fp8 tile into the
+    # bf16 stage layout it gathers native rows into, so it is bitwise the same
+    # kernel on the dequantized cache; split items merged in-kernel or not
+    _say(f"fp8 128-head items vs bf16 on dequantized cores={cores}")
+    kw = _fp8_case(lens=[4000, 2999, 3500, 2100], heads=128, k=2048, seed=6, sinks="uniform")
+    out8, lse8 = _run_items(kw, 128, core_num=cores)
+    out16, lse16 = _run_items(_dequant_kw(kw), 128, core_num=cores)
+    assert torch.equal(out8.cpu(), out16.reshape(out8.shape).cpu())
+    assert torch.equal(lse8.cpu(), lse16.reshape(lse8.shape).cpu())
+    _check(out8, lse8, kw)
+    out_s, lse_s = _run_items(kw, 128, core_num=cores, _separate_merge=True)
+    assert torch.equal(out8, out_s) and torch.equal(lse8, lse_s)
+
+
 @requires_gpu
 def test_fp8_bsnd_layout_and_uint8_inference():
     # kv_cache_dtype inferred from the uint8 cache; BSND layout
