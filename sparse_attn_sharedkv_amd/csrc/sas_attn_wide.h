@@ -470,27 +470,31 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         }
         dma16_vaddr(src, raw_base(tile) + (uint32_t)((w + NW * i) * 1024));
       };
-      // Raw tile t (landed and published by a barrier) into bf16 stage t % 2:
-      // thread x dequantizes dims 32 (x % 16) .. + 31 of tile row x / 16 as
-      // bf16(fp32(e4m3) * scale) and, for x % 16 < 8, copies rope chunk x % 16.
+      // Raw tile t (landed and published by a barrier) into bf16 stage t % 2 as
+      // bf16(fp32(e4m3) * scale): wave w converts rows w + 8 k (k < 4), lane l dims
+      // 8 l .. 8 l + 7 (consecutive lanes read consecutive 8-byte pieces and write
+      // consecutive 16-byte chunks: no bank conflicts); the first 256 threads copy
+      // the 32 x 8 rope chunks.
       auto convert = [&](int tile) {
-        // (the thread's index recomputed here, so no offset stays live across the loop)
-        const int x = 64 * w + lane_id_here();
-        const int r = x >> 4, j = x & 15;
-        const lds_p raw = (lds_p)(raw_base(tile) + (uint32_t)(r * SAS_FP8_ROW_BYTES));
+        typedef int i32x2 __attribute__((ext_vector_type(2)));
+        const int l = lane_id_here();  // (recomputed here: no offset stays live across the loop)
         const uint32_t st = kv_base + (uint32_t)((tile % 2) * STAGE_BYTES);
-        typedef i16x8 SAS_LDS* lds8;
-        lds8 dst = (lds8)(st + (uint32_t)(wide_row_base(r) + 64 * j));
-        const float sc8 = *(const float SAS_LDS*)(raw + LATENT_BYTES + 4 * (j >> 2));
+        const uint32_t rb = raw_base(tile);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {  // one 16-byte half at a time
-          const i32x4 v = *(const i32x4 SAS_LDS*)(raw + 32 * j + 16 * h);
-          dst[2 * h] = fp8x8_dequant_bf16(make_uint2((uint32_t)v[0], (uint32_t)v[1]), sc8);
-          dst[2 * h + 1] = fp8x8_dequant_bf16(make_uint2((uint32_t)v[2], (uint32_t)v[3]), sc8);
+        for (int k = 0; k < TILE / NW; ++k) {
+          const int r = w + NW * k;
+          const lds_p raw = (lds_p)(rb + (uint32_t)(r * SAS_FP8_ROW_BYTES));
+          const i32x2 v = *(const i32x2 SAS_LDS*)(raw + 8 * l);
+          const float sc8 = *(const float SAS_LDS*)(raw + LATENT_BYTES + 4 * (l >> 4));
+          *(i16x8 SAS_LDS*)(st + (uint32_t)(wide_row_base(r) + 16 * l)) =
+              fp8x8_dequant_bf16(make_uint2((uint32_t)v[0], (uint32_t)v[1]), sc8);
         }
-        if (j < 8) {
-          const i16x8 rp = *(const i16x8 SAS_LDS*)(raw + LATENT_BYTES + 16 + 16 * j);
-          *(lds8)(st + (uint32_t)(WMAIN + 16 * wide_rope_slot(wide_perm(r), j))) = rp;
+        const int x = 64 * w + l;
+        if (x < TILE * 8) {
+          const int r = x >> 3, c = x & 7;
+          const i16x8 rp = *(const i16x8 SAS_LDS*)(rb + (uint32_t)(r * SAS_FP8_ROW_BYTES +
+                                                                    LATENT_BYTES + 16 + 16 * c));
+          *(i16x8 SAS_LDS*)(st + (uint32_t)(WMAIN + 16 * wide_rope_slot(wide_perm(r), c))) = rp;
         }
       };
 
