@@ -150,6 +150,23 @@ __device__ inline void dma16_sbase(const void* sbase, uint32_t voff, uint32_t ld
       "s"(sbase), "s"(lds_base)
       : "memory");
 }
+// dma16_sbase on the lanes of `lanes` only (lane i still writes lds_base + 16 i):
+// exec is narrowed and restored inside the statement, so the compiler never sees
+// it change
+__device__ inline void dma16_sbase_lanes(const void* sbase, uint32_t voff, uint32_t lds_base,
+                                         uint64_t lanes) {
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %0, exec\n\t"
+      "s_mov_b64 exec, %4\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2 sc0 nt\n\t"
+      "s_mov_b64 exec, %0\n\t"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(lds_base), "s"(lanes)
+      : "memory");
+}
 __device__ inline void dma16_vaddr(const void* gptr, uint32_t lds_base) {
   asm volatile(
       "s_mov_b32 m0, %1\n\t"
@@ -2655,7 +2672,7 @@ extern "C" int sas_attention_launch_noalloc(const SasAttnArgs* a, void* stream) 
   return sas_attention_launch(&b, stream);
 }
 
-extern "C" int sas_version(void) { return 112; }
+extern "C" int sas_version(void) { return 113; }
 
 extern "C" int sas_args_struct_size(void) { return (int)sizeof(SasAttnArgs); }
 

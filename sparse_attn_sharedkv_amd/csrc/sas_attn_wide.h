@@ -35,6 +35,7 @@
 #define SAS_WVPF 3  // Vᵀ operands in flight per wave (wide_kernel)
 #endif
 
+
 namespace sas {
 
 // LDS stage layout of the wide kernel (one 32-row tile).
@@ -107,12 +108,13 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   constexpr int STAGE_BYTES = WMAIN + (ROPE ? WROPE : 0);
   constexpr int RAW_CH = SAS_FP8_ROW_BYTES / 16;  // 16-byte chunks per fp8 row (41)
   constexpr int LATENT_BYTES = 512;      // fp8 row: e4m3 dims 0..511, then 4 fp32 scales, rope
-  constexpr int RAW_DMA = 3;             // fp8: raw DMA instructions per wave and tile (24 x 1 KB)
-  constexpr int RAW_STAGE = RAW_DMA * NW * 1024;  // 32 rows x 656 B (1312 chunks), padded
+  constexpr int RAW_DMA = TILE / NW;     // fp8: raw DMA instructions per wave and tile, a row each
+  constexpr uint64_t RAW_LANES = (1ull << RAW_CH) - 1;  // the lanes of a row's DMA (0 .. 40)
+  constexpr int RAW_STAGE = TILE * SAS_FP8_ROW_BYTES;   // 32 rows x 656 B
   constexpr int NRAW = FP8 ? 3 : 0;      // raw ring depth
   constexpr int LDS_BYTES = NSTG * STAGE_BYTES + NRAW * RAW_STAGE;
   static_assert(!FP8 || (DQK == 576 && __is_same(T, __bf16)), "fp8 rows: d_qk 576, bf16");
-  static_assert(TILE * RAW_CH <= RAW_DMA * NW * 64, "raw stage chunks");
+  static_assert(RAW_CH <= 64 && RAW_CH * 16 == SAS_FP8_ROW_BYTES, "one fp8 row per DMA");
   constexpr int RPW = TILE / NW;         // main-part DMA instructions per wave and tile (4)
   constexpr int NROPE = ROPE ? TILE / 8 : 0;  // rope DMA instructions per tile (waves w < 4)
   constexpr int RCH = 1024;              // positions resolved into LDS at a time
@@ -455,47 +457,53 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         return (lds_p)(kv_base + (uint32_t)((tile % NSTG) * STAGE_BYTES));
       };
       // ---- fp8 rows: raw DMA and dequantization ----
-      // Raw tile t goes to raw stage t % 3: this wave's instruction i fills
-      // chunks 64 (w + 8 i) + lane of the stage, chunk c being 16-byte piece
-      // c % 41 of tile row c / 41 (chunks past the tile read the zero row).
+      // Raw tile t goes to raw stage t % 3 as 32 rows of 656 bytes: this wave's
+      // instruction j copies row w + 8 j whole, lane i < 41 its 16-byte piece i,
+      // from the row's address (lane j of raw_addrs, read into scalars) plus 16 i.
+      // Past the chunk's last tile the rows are read from the zero row.
       auto raw_base = [&](int tile) -> uint32_t {
         return kv_base + (uint32_t)(NSTG * STAGE_BYTES + (tile % 3) * RAW_STAGE);
       };
-      auto raw_issue = [&](int tile, int i) {
-        const int c = 64 * (w + NW * i) + lane_id_here();
-        const char* src = (const char*)g_zero_row;
-        if (tile < ntile && c < TILE * RAW_CH) {
-          const int r = c / RAW_CH;
-          src = row_ptr(rowid[tile * TILE + r]) + 16 * (c - r * RAW_CH);
-        }
-        dma16_vaddr(src, raw_base(tile) + (uint32_t)((w + NW * i) * 1024));
+      auto raw_addrs = [&](int tile) -> uint64_t {
+        const bool real = tile < ntile;
+        const int l = lane_id_here();
+        const uint32_t id = rowid[(real ? tile : 0) * TILE + w + NW * (l < RAW_DMA ? l : 0)];
+        return (uint64_t)(uintptr_t)(real ? row_ptr(id) : (const char*)g_zero_row);
+      };
+      auto raw_issue = [&](uint64_t ra, uint32_t voff, int tile, int j) {
+        dma16_sbase_lanes(lane_row(ra, j), voff,
+                          raw_base(tile) + (uint32_t)((w + NW * j) * SAS_FP8_ROW_BYTES), RAW_LANES);
       };
       // Raw tile t (landed and published by a barrier) into bf16 stage t % 2 as
       // bf16(fp32(e4m3) * scale): wave w converts rows w + 8 k (k < 4), lane l dims
       // 8 l .. 8 l + 7 (consecutive lanes read consecutive 8-byte pieces and write
       // consecutive 16-byte chunks: no bank conflicts); the first 256 threads copy
       // the 32 x 8 rope chunks.
-      auto convert = [&](int tile) {
+      auto convert_row = [&](int tile, int k) {
         typedef int i32x2 __attribute__((ext_vector_type(2)));
         const int l = lane_id_here();  // (recomputed here: no offset stays live across the loop)
         const uint32_t st = kv_base + (uint32_t)((tile % 2) * STAGE_BYTES);
-        const uint32_t rb = raw_base(tile);
-#pragma unroll
-        for (int k = 0; k < TILE / NW; ++k) {
-          const int r = w + NW * k;
-          const lds_p raw = (lds_p)(rb + (uint32_t)(r * SAS_FP8_ROW_BYTES));
-          const i32x2 v = *(const i32x2 SAS_LDS*)(raw + 8 * l);
-          const float sc8 = *(const float SAS_LDS*)(raw + LATENT_BYTES + 4 * (l >> 4));
-          *(i16x8 SAS_LDS*)(st + (uint32_t)(wide_row_base(r) + 16 * l)) =
-              fp8x8_dequant_bf16(make_uint2((uint32_t)v[0], (uint32_t)v[1]), sc8);
-        }
-        const int x = 64 * w + l;
+        const int r = w + NW * k;
+        const lds_p raw = (lds_p)(raw_base(tile) + (uint32_t)(r * SAS_FP8_ROW_BYTES));
+        const i32x2 v = *(const i32x2 SAS_LDS*)(raw + 8 * l);
+        const float sc8 = *(const float SAS_LDS*)(raw + LATENT_BYTES + 4 * (l >> 4));
+        *(i16x8 SAS_LDS*)(st + (uint32_t)(wide_row_base(r) + 16 * l)) =
+            fp8x8_dequant_bf16(make_uint2((uint32_t)v[0], (uint32_t)v[1]), sc8);
+      };
+      auto convert_rope = [&](int tile) {
+        const int x = 64 * w + lane_id_here();
         if (x < TILE * 8) {
           const int r = x >> 3, c = x & 7;
-          const i16x8 rp = *(const i16x8 SAS_LDS*)(rb + (uint32_t)(r * SAS_FP8_ROW_BYTES +
+          const i16x8 rp = *(const i16x8 SAS_LDS*)(raw_base(tile) + (uint32_t)(r * SAS_FP8_ROW_BYTES +
                                                                     LATENT_BYTES + 16 + 16 * c));
-          *(i16x8 SAS_LDS*)(st + (uint32_t)(WMAIN + 16 * wide_rope_slot(wide_perm(r), c))) = rp;
+          *(i16x8 SAS_LDS*)(kv_base + (uint32_t)((tile % 2) * STAGE_BYTES + WMAIN +
+                                                  16 * wide_rope_slot(wide_perm(r), c))) = rp;
         }
+      };
+      auto convert = [&](int tile) {
+#pragma unroll
+        for (int k = 0; k < TILE / NW; ++k) convert_row(tile, k);
+        convert_rope(tile);
       };
 
       auto mma16 = [&](i16x8 x, i16x8 y, f32x4 c) -> f32x4 {
@@ -508,7 +516,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
 
       // ---- Q·Kᵀ of one tile: two row blocks (independent accumulators,
       // alternating), K operands KPF MFMAs ahead ----
-      auto qk_tile = [&](lds_p sb, f32x4& s0, f32x4& s1) {
+      auto qk_tile = [&](lds_p sb, f32x4& s0, f32x4& s1, auto&& hook) {
         constexpr int NQK = 2 * NKS;
         constexpr int KPF = SAS_WKPF;
         const lds_p kb_main = sb + wide_k_main(lane_id_here());
@@ -536,6 +544,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
           if (i + KPF < NQK) kb[i % KPF] = *kaddr(i + KPF);
           if (i & 1) s1 = mma16(op, qf[i >> 1], s1);
           else s0 = mma16(op, qf[i >> 1], s0);
+          hook(i);
           __builtin_amdgcn_sched_barrier(0);
         }
       };
@@ -611,18 +620,18 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         i16x8 vb[VPF];
 #pragma unroll
         for (int i = 0; i < VPF; ++i) vb[i] = vop(i);
+        const uint32_t voff = FP8 ? 16u * (uint32_t)lane_id_here() : 0u;
 #pragma unroll
         for (int d = 0; d < NDV; ++d) {
           const i16x8 op = vb[d % VPF];
           if (d + VPF < NDV) vb[d % VPF] = vop(d + VPF);
           acc[d] = mma16(op, pk, acc[d]);
           if constexpr (FP8) {
-            // the raw DMAs of tile t + 3 (into the raw stage tile t held), and
-            // tile t + 1's dequantization into the bf16 stage tile t - 1 held
+            // the raw DMAs of tile t + 3 (into the raw stage tile t held; dd.main
+            // holds their row addresses)
 #pragma unroll
             for (int j = 0; j < RAW_DMA; ++j)
-              if (d == 3 + 6 * j) raw_issue(t + 3, j);
-            if (d == 20 && t + 1 < ntile) convert(t + 1);
+              if (d == 3 + 8 * j) raw_issue(dd.main, voff, t + 3, j);
           } else {
 #pragma unroll
             for (int j = 0; j < DMA_MAX; ++j)
@@ -633,10 +642,13 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
 
       // ---- prologue: tiles 0, 1, 2 in flight, then the query fragment ----
       if constexpr (FP8) {
+        const uint32_t voff = 16u * (uint32_t)lane;
 #pragma unroll
-        for (int tt = 0; tt < 3; ++tt)
+        for (int tt = 0; tt < 3; ++tt) {
+          const uint64_t ra = raw_addrs(tt);
 #pragma unroll
-          for (int j = 0; j < RAW_DMA; ++j) raw_issue(tt, j);
+          for (int j = 0; j < RAW_DMA; ++j) raw_issue(ra, voff, tt, j);
+        }
       } else {
         issue(next_addrs(0));
         issue(next_addrs(1));
@@ -669,11 +681,25 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         else wait_all_but(std::integral_constant<int, 2>{});  // this wave's share of tile t
         __syncthreads();                                       // barrier t
         f32x4 s0, s1;
-        qk_tile(sb, s0, s1);
+        // (fp8 rows: tile t + 1 is dequantized into the bf16 stage tile t - 1 held,
+        // a row at a time between the Q·Kᵀ MFMAs, whose matrix-core time the
+        // conversion's VALU work runs beside)
+        qk_tile(sb, s0, s1, [&](int i) {
+          if constexpr (FP8) {
+            if (t + 1 < ntile) {
+#pragma unroll
+              for (int k = 0; k < TILE / NW; ++k)
+                if (i == 4 + 8 * k) convert_row(t + 1, k);
+              if (i == 33) convert_rope(t + 1);
+            }
+          }
+        });
         float alpha;
         const i16x8 pk = softmax_tile(t, s0, s1, alpha);
         if constexpr (FP8) {
-          pv_tile(sb, pk, alpha, DmaAddrs{}, t);
+          DmaAddrs dd;
+          dd.main = raw_addrs(t + 3);
+          pv_tile(sb, pk, alpha, dd, t);
         } else {
           const DmaAddrs dd = next_addrs(t + 3);
           pv_tile(sb, pk, alpha, dd, t);
