@@ -281,7 +281,7 @@ def main():
     achieved = nbytes / (attn_avg * 1e-3) / 1e9
     # items of 128 heads run on the 128-head kernel (either row format); smaller
     # items on the pipelined kernel for fp8 rows, else the one-wave-per-SIMD kernel
-    kernel = ("sas::wide_kernel" if preps[0].args.m_base == 128
+    kernel = ("sas::wide_kernel" if preps[0].args.m_base == 128 or api.uses_row_pairs(preps[0])
               else "sas::attn3_kernel" if sets[0].get("kv_cache_dtype") else "sas::attn2_kernel")
     if w.get("prefill"):
         # prefill: consecutive query rows re-read each other's cache rows, which

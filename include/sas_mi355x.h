@@ -185,7 +185,14 @@ typedef struct SasAttnArgs {
    * dims stay bf16. P·V stays on the dequantized bf16 rows. No reference counterpart
    * (kernel.py:2036-2352 forms Q·Kᵀ in bf16): it adds the query's quantization error,
    * which is small against golden for N(0,1)-scaled data but not for the reference
-   * tests' U(-10, 10) data, so it is opt-in. */
+   * tests' U(-10, 10) data, so it is opt-in.
+   * SAS_PHASE_ROW_ITEMS (bit 4, native rows) turns off row pairs: by default a launch
+   * whose sequences hold several query rows, with items of 64 heads (num_heads <= 64),
+   * no split items (num_fd == 0 and num_partial_slots == 0) and scenario 1 or 2, runs
+   * two consecutive query rows per workgroup on the 128-head kernel over the union of
+   * their attended rows (prefill: the two windows share all but two rows). No
+   * reference counterpart (the reference's prefill task is one query row,
+   * kernel.py:262, :293); results agree with the one-row items to within rounding. */
   int32_t phases;
   /* row format of ori_kv and cmp_kv: SAS_KV_NATIVE or SAS_KV_FP8_DS_MLA */
   int32_t kv_format;
@@ -222,6 +229,7 @@ int sas_attention_launch(const SasAttnArgs* args, void* stream);
  * streams, concurrent threads) race and must be serialised by the caller. */
 #define SAS_PHASE_PIPELINED 4
 #define SAS_PHASE_FP8_QK 8
+#define SAS_PHASE_ROW_ITEMS 16
 #define SAS_NOALLOC_SCRATCH_BYTES (72ull << 20)
 int sas_attention_launch_noalloc(const SasAttnArgs* args, void* stream);
 

@@ -35,6 +35,7 @@ KV_FP8_DS_MLA = 1
 FP8_ROW_BYTES = 656
 SAS_PHASE_PIPELINED = 4        # SasAttnArgs.phases bit: native rows through the pipelined kernel
 SAS_PHASE_FP8_QK = 8           # SasAttnArgs.phases bit: fp8 rows, Q·Kᵀ on fp8 MFMA (e4m3 queries)
+SAS_PHASE_ROW_ITEMS = 16       # SasAttnArgs.phases bit: no row pairs (one query row per item)
 SCHED_DEVICE = -1             # SasAttnArgs.num_fd: schedule summary read on the device
 MERGE_SYNC_WORDS = 2 * AIC_CORE_NUM  # SasAttnArgs.merge_sync: uint64 arrival counters
 DEV_SCHED_MAX_BATCH = 4096

@@ -180,7 +180,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
             fp8_qk: bool = False,
             _stream_schedule: bool = False,
             _pipelined: bool = False, _separate_merge: Optional[bool] = None,
-            _m_base: Optional[int] = None) -> Prepared:
+            _m_base: Optional[int] = None, _row_items: bool = False) -> Prepared:
     """Validate and stage one call (host work of api.py:186-384) without launching.
 
     ``schedule``: ``"host"`` reads the lengths back and schedules on the CPU (the
@@ -197,6 +197,8 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     kernel, False inside it; None (default) inside it when no item has more than
     ``MERGE_IN_KERNEL_MAX_PIECES`` pieces. ``_m_base`` (tests, timing): heads per item instead
     of ``m_base_for``'s choice (a call with its own ``metadata`` uses the metadata's).
+    ``_row_items`` (tests, timing): one query row per workgroup item even where the
+    library would pair consecutive rows (``SAS_PHASE_ROW_ITEMS``).
     """
     del seqused_q  # API-parity placeholder (api.py:186)
     assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
@@ -426,9 +428,22 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     return Prepared(args=a, keep=keep, out=out, lse=lse, layout_q=layout_q,
                     bsnd_shape=None if layout_q == "TND" else (nb, total // max(nb, 1), n1, dv),
                     device=dev, phase_bits=(_lib.SAS_PHASE_FP8_QK if fp8_qk else 0) |
-                    (_lib.SAS_PHASE_PIPELINED if _pipelined else 0),
+                    (_lib.SAS_PHASE_PIPELINED if _pipelined else 0) |
+                    (_lib.SAS_PHASE_ROW_ITEMS if _row_items else 0),
                     merge_in_kernel=few_pieces if _separate_merge is None
                     else not _separate_merge)
+
+
+def uses_row_pairs(prep: Prepared) -> bool:
+    """Whether the library runs this call as row pairs (two consecutive query rows
+    of 64 heads per workgroup on the 128-head kernel): the rule of the library's
+    launch (native rows, items of 64 heads with at most 64 heads, no split items,
+    scenarios 1 and 2, several query rows in some sequence)."""
+    a = prep.args
+    return (a.kv_format == _lib.KV_NATIVE and a.num_fd == 0 and a.num_partial_slots == 0
+            and a.m_base == 64 and a.num_heads <= 64 and a.scenario <= 2
+            and a.total_tokens > a.batch
+            and not (prep.phase_bits & (_lib.SAS_PHASE_ROW_ITEMS | _lib.SAS_PHASE_PIPELINED)))
 
 
 def launch(prep: Prepared, stream: Optional[torch.cuda.Stream] = None, phases: int = 0) -> None:

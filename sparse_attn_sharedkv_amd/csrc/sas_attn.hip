@@ -2436,6 +2436,17 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
   }
 }
 
+// Launches whose sequences hold several query rows run two consecutive rows of
+// 64 heads per workgroup on the 128-head kernel when no item is split (the host
+// schedule has no merge tasks and no partial slots) and each row attends a window
+// and / or a dense compressed prefix: the two rows' lists then overlap in all but
+// a position or two, so one gathered tile serves both.
+static bool row_pairs_ok(const SasAttnArgs& a) {
+  return !(a.phases & SAS_PHASE_ROW_ITEMS) && a.kv_format == SAS_KV_NATIVE && a.num_fd == 0 &&
+         a.num_partial_slots == 0 && a.scenario <= 2 && a.num_heads <= 64 && a.m_base == 64 &&
+         a.total_tokens > a.batch;
+}
+
 template <int DQK, int NHG, typename T, int KVF>
 static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
   const int phases = (a.phases & 3) == 0 ? 3 : (a.phases & 3);
@@ -2460,6 +2471,9 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
       if (a.phases & SAS_PHASE_PIPELINED)
         hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF>), dim3(8 * per_xcd),
                            dim3(256 * NHG), 0, st, a);
+      else if (NHG == 2 && row_pairs_ok(a))  // two query rows of 64 heads per workgroup
+        hipLaunchKernelGGL((wide_kernel<DQK, 512, T, SAS_KV_NATIVE, true>), dim3(8 * per_xcd),
+                           dim3(512), 0, st, a);
       else if (a.total_tokens > a.batch)  // some batch holds several query rows
         hipLaunchKernelGGL((attn2_kernel<DQK, 512, NHG, T, KVF, true>), dim3(8 * per_xcd),
                            dim3(128 * NHG), 0, st, a);
@@ -2551,8 +2565,8 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     set_error("sas_attention_launch: scenario inputs missing");
     return SAS_E_INVALID;
   }
-  if (a->phases < 0 || a->phases > 15) {
-    set_error("sas_attention_launch: phases must be 0..15");
+  if (a->phases < 0 || a->phases > 31) {
+    set_error("sas_attention_launch: phases must be 0..31");
     return SAS_E_INVALID;
   }
   if ((a->phases & SAS_PHASE_FP8_QK) && a->kv_format != SAS_KV_FP8_DS_MLA) {

@@ -90,10 +90,16 @@ __device__ inline int wide_rope1(int l) {
 }
 __device__ inline int wide_v(int l) { return wide_row_base(4 * (l >> 4) + ((l & 15) >> 2)) + 8 * (l & 3); }
 
-template <int DQK, int DV, typename T, int KVF = SAS_KV_NATIVE>
+template <int DQK, int DV, typename T, int KVF = SAS_KV_NATIVE, bool PAIR = false>
 __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   constexpr int NW = 8;                  // waves per workgroup
-  constexpr int MB = 128;                // heads per item (m-block)
+  constexpr int MB = 128;                // query heads per workgroup (columns of Sᵀ)
+  // PAIR: items of 64 heads (at most 64 heads, one head block), two consecutive
+  // query rows of a sequence at a time — waves 0..3 take row s, waves 4..7 row
+  // s + 1, over the union of the two rows' positions, each wave masking the
+  // positions its own row does not attend. Only for schedules without split
+  // items, windows and dense compressed prefixes (scenarios 1, 2).
+  constexpr int IMB = PAIR ? 64 : MB;    // heads per item (m-block)
   constexpr int NT = 64 * NW;            // threads
   constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
   // fp8 rows (SAS_KV_FP8_DS_MLA): tiles arrive by DMA as raw 656-byte rows in a
@@ -114,6 +120,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   constexpr int NRAW = FP8 ? 3 : 0;      // raw ring depth
   constexpr int LDS_BYTES = NSTG * STAGE_BYTES + NRAW * RAW_STAGE;
   static_assert(!FP8 || (DQK == 576 && __is_same(T, __bf16)), "fp8 rows: d_qk 576, bf16");
+  static_assert(!(PAIR && FP8), "row pairs: native rows");
   static_assert(RAW_CH <= 64 && RAW_CH * 16 == SAS_FP8_ROW_BYTES, "one fp8 row per DMA");
   constexpr int RPW = TILE / NW;         // main-part DMA instructions per wave and tile (4)
   constexpr int NROPE = ROPE ? TILE / 8 : 0;  // rope DMA instructions per tile (waves w < 4)
@@ -137,7 +144,9 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15;
   const int g4 = lane >> 4;                // 16-lane group
-  const int hlocal = 16 * w + r16;         // head within the item's m-block
+  const int srow = 16 * w + r16;           // the lane's column (staging row) in the workgroup
+  const int gsel = PAIR ? (w >> 2) : 0;    // row pairs: which of the two rows
+  const int hlocal = PAIR ? srow & 63 : srow;  // head within the item's m-block
   const bool has_rope = ROPE && w < NROPE; // this wave issues rope DMA instruction w
   int s2b = a.s2_base;
   int nfa = a.num_fa;
@@ -189,7 +198,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   asm volatile("" ::"v"(lane_aq), "v"(lane_kv), "v"(lane_qp));
   int item_par = 0;  // which first_neg slot the next top-k scan uses
   bool first_item = true;
-  const int hblocks = (a.num_heads + MB - 1) / MB;
+  const int hblocks = (a.num_heads + IMB - 1) / IMB;
   auto batch_lens = [&](int bb, int& aq, int& akv, int& qp) {
     const int bc = bb < a.batch ? bb : a.batch - 1;
     if (lens_in_lanes) {
@@ -217,22 +226,57 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
     const bool is_end = (b == b_end && m == s_end);
     const int s = m / hblocks;
     const int hb = m - s * hblocks;
-    const int head = hb * MB + hlocal;
-    const bool head_ok = head < a.num_heads;
+    const int head = hb * IMB + hlocal;
     if (is_end && j_end == 0) break;
 
     const int tok = qpre + s;
-    const ItemGeom g =
-        item_geom(act_q, act_kv, s, a.ori_win_left, a.scenario, a.cmp_ratio, a.topk);
+    const bool partial = (first_item && j_start > 0) || is_end;
+    ItemGeom g = item_geom(act_q, act_kv, s, a.ori_win_left, a.scenario, a.cmp_ratio, a.topk);
+    // row pairs: the next row joins when neither row is a piece of a split item,
+    // and g becomes the union of the two rows' lists (the window rows of row
+    // s + 1 start at or after those of row s, and the two windows touch)
+    bool pair = false;
+    ItemGeom gA = g, gB = g;
+    if constexpr (PAIR) {
+      if (!partial && hblocks == 1 && a.scenario <= 2 && m + 1 < act_q &&
+          !(b == b_end && m + 1 >= s_end)) {
+        gB = item_geom(act_q, act_kv, s + 1, a.ori_win_left, a.scenario, a.cmp_ratio, a.topk);
+        const int hiA = gA.win_lo + gA.n_win, hiB = gB.win_lo + gB.n_win;
+        if (gA.n_win == 0 && gB.n_win == 0) {
+          pair = true;
+        } else if (gA.n_win > 0 && gB.n_win > 0 && gB.win_lo >= gA.win_lo && gB.win_lo <= hiA) {
+          pair = true;
+          g.n_win = (hiB > hiA ? hiB : hiA) - gA.win_lo;
+        }
+        if (pair) {
+          g.thr = gB.thr > gA.thr ? gB.thr : gA.thr;
+          g.n_cmp = gB.n_cmp > gA.n_cmp ? gB.n_cmp : gA.n_cmp;
+        }
+      }
+    }
+    // this wave's row: its token, whether its head is real, and where its own
+    // positions lie in the list g (window part [wlo, whi), compressed [clo, chi))
+    const int tok_w = tok + (pair ? gsel : 0);
+    const bool head_ok = head < a.num_heads && (gsel == 0 || pair);
+    int wlo = 0, whi = 0, clo = 0, chi = 0;
+    if constexpr (PAIR) {
+      if (gsel == 0 || pair) {
+        const ItemGeom& gg = gsel ? gB : gA;
+        wlo = gg.win_lo - g.win_lo;
+        whi = wlo + gg.n_win;
+        clo = g.n_win;
+        chi = g.n_win + gg.n_cmp;
+      }
+    }
     const int L = g.n_win + g.n_cmp;
     const int nblk = (L + s2b - 1) / s2b;
     const int blo = first_item ? j_start : 0;
     int bhi = is_end ? j_end : nblk;
     if (bhi > nblk) bhi = nblk;
-    const bool partial = (first_item && j_start > 0) || is_end;
     const int p_lo = blo * s2b;
     const int p_hi = bhi * s2b < L ? bhi * s2b : L;
     const bool tok_ok = tok >= 0 && tok < a.total_tokens;
+    const bool tok_ok_w = tok_w >= 0 && tok_w < a.total_tokens;
 
     // ---- online-softmax state of this lane's head (golden.py:156-160 seeds m =
     // sink, l = 1; the 1 goes to the lanes of group 0, whose row sums are added to
@@ -272,9 +316,9 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       // past num_heads or a token out of range reads token 0's first heads: its
       // scores only reach its own softmax column and output row, never stored.
       auto load_q = [&]() {
-        const bool ok = tok_ok && head_ok;
+        const bool ok = tok_ok_w && head_ok;
         const short* qrow =
-            (const short*)a.q + ((size_t)(ok ? tok : 0) * a.num_heads + (ok ? head : 0)) * DQK;
+            (const short*)a.q + ((size_t)(ok ? tok_w : 0) * a.num_heads + (ok ? head : 0)) * DQK;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) qf[ks] = *(const i16x8*)(qrow + 32 * ks + 8 * g4);
       };
@@ -554,7 +598,16 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       auto softmax_tile = [&](int t, f32x4 s0, f32x4 s1, float& alpha) -> i16x8 {
         // (masking only on tiles with invalid rows: tile tails, -1 / out-of-range
         // ids; the empty asm keeps this a branch, so full tiles skip the selects)
-        const uint32_t tm = tmask[t];
+        uint32_t tm = tmask[t];
+        if constexpr (PAIR) {
+          // positions of the tile outside this wave's row's own list
+          auto span = [](int lo, int hi, int p0) -> uint32_t {
+            const int x = lo - p0 > 0 ? lo - p0 : 0, y = hi - p0 < TILE ? hi - p0 : TILE;
+            return y > x ? (uint32_t)(((1ull << y) - 1) & ~((1ull << x) - 1)) : 0u;
+          };
+          const int p0 = c0 + TILE * t;
+          tm &= span(wlo, whi, p0) | span(clo, chi, p0);
+        }
         if (__builtin_amdgcn_readfirstlane(tm) != 0xFFFFFFFFu) {
           asm volatile("");
           const uint32_t v0 = tm >> (4 * g4), v1 = tm >> (16 + 4 * g4);
@@ -726,7 +779,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       const int nh = min(MB, a.num_heads - hb * MB);  // heads of this item
       constexpr int SROW = DV * 2 + 16;  // staging row stride (bytes; 16-byte aligned rows)
       constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
-      int tid_e = tid, hl_e = hlocal, dv_e = 4 * g4;
+      int tid_e = tid, hl_e = srow, dv_e = 4 * g4;
       asm volatile("" : "+v"(tid_e), "+v"(hl_e), "+v"(dv_e));
       if (!partial) {
         const float inv = 1.0f / l_run;
@@ -738,15 +791,26 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         }
         __syncthreads();
         if (tok_ok) {
-          char* obase = (char*)((T*)a.out + ((size_t)tok * a.num_heads + hb * MB) * DV);
-          for (int c = tid_e; c < nh * CPR; c += NT) {
-            const int h = c / CPR, c16 = c - h * CPR;
-            *(i16x8*)(obase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
+          if constexpr (PAIR) {
+            // staging row h: row s + h / 64, head h % 64
+            char* obase = (char*)((T*)a.out + (size_t)tok * a.num_heads * DV);
+            for (int c = tid_e; c < (pair ? 2 : 1) * 64 * CPR; c += NT) {
+              const int h = c / CPR, c16 = c - h * CPR;
+              if ((h & 63) < a.num_heads && tok + (h >> 6) < a.total_tokens)
+                *(i16x8*)(obase + ((size_t)(h >> 6) * a.num_heads + (h & 63)) * DV * 2 + c16 * 16) =
+                    *(const i16x8*)(stg + h * SROW + c16 * 16);
+            }
+          } else {
+            char* obase = (char*)((T*)a.out + ((size_t)tok * a.num_heads + hb * MB) * DV);
+            for (int c = tid_e; c < nh * CPR; c += NT) {
+              const int h = c / CPR, c16 = c - h * CPR;
+              *(i16x8*)(obase + (size_t)h * DV * 2 + c16 * 16) = *(const i16x8*)(stg + h * SROW + c16 * 16);
+            }
           }
-          if (g4 == 0 && head_ok)
-            a.lse[(size_t)tok * a.num_heads + head] = (m_run + __log2f(l_run)) * LN2;
+          if (g4 == 0 && head_ok && tok_ok_w)
+            a.lse[(size_t)tok_w * a.num_heads + head] = (m_run + __log2f(l_run)) * LN2;
         }
-      } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
+      } else if (!PAIR && slot >= 0 && slot < a.num_partial_slots && a.workspace) {
         // fp16 partials (acc / l, scaled): the head's whole row sits in its four
         // lanes, whose max picks the scale
         const bool empty = !(l_run > 0.0f);
@@ -804,7 +868,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         }
       }
     }
-    if (partial && merge_here) {
+    if (!PAIR && partial && merge_here) {
       // the piece that completes the item merges it (bit-identical to merge_kernel)
       const int slot0 = (first_item && j_start > 0) ? slot - cont_k : slot;
       if (slot0 >= 0 && slot < a.num_partial_slots && slot0 < SAS_MERGE_SYNC_WORDS) {
@@ -815,6 +879,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
     if (partial) ++slot;
     if (is_end) break;
     first_item = false;
+    if (pair) ++m;
     ++m;
   }
 }

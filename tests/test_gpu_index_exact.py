@@ -156,6 +156,11 @@ def _check(kw, idx, t1, t2, scenario, ratio, bs1, bs2, **extra):
     dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
     out, lse = sparse_attn_sharedkv(**dev, return_softmax_lse=True, **extra)
     torch.cuda.synchronize()
+    _verify(kw, idx, t1, t2, scenario, ratio, bs1, bs2, out, lse)
+
+
+def _verify(kw, idx, t1, t2, scenario, ratio, bs1, bs2, out, lse):
+    """Every token's gathered multiset (from out and lse) against the oracle's resolution."""
     heads = kw["q"].shape[-2]
     out = out.reshape(-1, heads, 512).float().cpu()
     lse = lse.reshape(-1, heads).cpu()
