@@ -272,7 +272,7 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     kv_fmt = _kv_format(kv_cache_dtype, ori_kv)
     fp8_rows = kv_fmt == _lib.KV_FP8_DS_MLA
     # items of at most 64 heads: the fp8 Q·Kᵀ form and the pipelined kernel (m_base_for)
-    item64 = bool(fp8_qk) or _pipelined
+    item64 = _pipelined
     m_base = m_base_for(int(n1), item64, nb) if _m_base is None else int(_m_base)
     if not m_base_valid(int(n1), item64, m_base):
         raise ValueError(f"no kernel for items of {m_base} heads at {n1} heads")

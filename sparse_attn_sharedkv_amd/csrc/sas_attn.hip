@@ -2456,7 +2456,11 @@ static hipError_t launch_attn(const SasAttnArgs& a, hipStream_t st) {
     // two-waves-per-SIMD kernel, whose second wave hides the dequantization
     if constexpr (KVF == SAS_KV_FP8_DS_MLA && NHG == 4) {
       // 128-head items of fp8 rows: the 128-head kernel, dequantizing a raw ring
-      hipLaunchKernelGGL((wide_kernel<DQK, 512, T, KVF>), dim3(8 * per_xcd), dim3(512), 0, st, a);
+      if (a.phases & SAS_PHASE_FP8_QK)
+        hipLaunchKernelGGL((wide_kernel<DQK, 512, T, KVF, false, true>), dim3(8 * per_xcd),
+                           dim3(512), 0, st, a);
+      else
+        hipLaunchKernelGGL((wide_kernel<DQK, 512, T, KVF>), dim3(8 * per_xcd), dim3(512), 0, st, a);
     } else if constexpr (KVF == SAS_KV_FP8_DS_MLA) {
       if (a.phases & SAS_PHASE_FP8_QK)
         hipLaunchKernelGGL((attn3_kernel<DQK, 512, NHG, T, KVF, true>), dim3(8 * per_xcd),
@@ -2548,15 +2552,14 @@ extern "C" int sas_attention_launch(const SasAttnArgs* a, void* stream) {
     return SAS_E_UNSUPPORTED;
   }
   // heads per item: 32 up to 32 heads, 64 up to 64 heads, above that 128 (one item
-  // holds the token's every head: the 128-head kernel) or 64; 64 only for the fp8
-  // Q·Kᵀ form (SAS_PHASE_FP8_QK) and for native rows run through the pipelined
-  // kernel (SAS_PHASE_PIPELINED)
-  const bool item64 = (a->phases & SAS_PHASE_FP8_QK) || (a->phases & SAS_PHASE_PIPELINED);
+  // holds the token's every head: the 128-head kernel) or 64; 64 only for native
+  // rows run through the pipelined kernel (SAS_PHASE_PIPELINED)
+  const bool item64 = (a->phases & SAS_PHASE_PIPELINED) != 0;
   const int want_mb = a->num_heads <= 32 ? 32 : (a->num_heads <= 64 || item64) ? 64 : 128;
   // above 64 heads items may also hold 64 heads (two per token)
   if (a->m_base != want_mb && !(want_mb == 128 && a->m_base == 64)) {
     set_error("sas_attention_launch: m_base must be 32 for <= 32 heads, 64 for <= 64 heads "
-              "(or SAS_PHASE_FP8_QK, or SAS_PHASE_PIPELINED), else 128 or 64");
+              "(or SAS_PHASE_PIPELINED), else 128 or 64");
     return SAS_E_INVALID;
   }
   if (a->scenario < 1 || a->scenario > 3 || (a->scenario >= 2 && (!a->cmp_kv ||
@@ -2686,7 +2689,7 @@ extern "C" int sas_attention_launch_noalloc(const SasAttnArgs* a, void* stream) 
   return sas_attention_launch(&b, stream);
 }
 
-extern "C" int sas_version(void) { return 113; }
+extern "C" int sas_version(void) { return 114; }
 
 extern "C" int sas_args_struct_size(void) { return (int)sizeof(SasAttnArgs); }
 

@@ -90,7 +90,7 @@ __device__ inline int wide_rope1(int l) {
 }
 __device__ inline int wide_v(int l) { return wide_row_base(4 * (l >> 4) + ((l & 15) >> 2)) + 8 * (l & 3); }
 
-template <int DQK, int DV, typename T, int KVF = SAS_KV_NATIVE, bool PAIR = false>
+template <int DQK, int DV, typename T, int KVF = SAS_KV_NATIVE, bool PAIR = false, bool QK8 = false>
 __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   constexpr int NW = 8;                  // waves per workgroup
   constexpr int MB = 128;                // query heads per workgroup (columns of Sᵀ)
@@ -106,21 +106,27 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   // ring of their own and are dequantized into the bf16 stage layout one tile
   // ahead of their use (the same bf16 values the native path computes on)
   constexpr bool FP8 = KVF == SAS_KV_FP8_DS_MLA;
+  // QK8 (fp8 rows, SAS_PHASE_FP8_QK): Q·Kᵀ on v_mfma_f32_16x16x128_f8f6f4 straight
+  // from the raw ring (e4m3 K blocks, bf16 rope) with the query quantized per head,
+  // the block scales applied to the four block dot products; P·V on the dequantized
+  // bf16 stage as in the bf16 form. The raw tile is read until its Q·Kᵀ is done, so
+  // the raw ring holds one tile more, and the bf16 stages drop their rope part.
   constexpr int ROWB = FP8 ? SAS_FP8_ROW_BYTES : DQK * 2;  // bytes per cache row in HBM
   constexpr int NKS = DQK / 32;          // 16x16x32 k-steps over d_qk (18 or 16)
   constexpr int NKS_MAIN = 16;           // k-steps over the 512 main dims
   constexpr int NDV = DV / 16;           // 16-wide dv blocks (32)
   constexpr int NSTG = FP8 ? 2 : 4;      // bf16 ring depth (fp8: the tile in use, the one filled)
-  constexpr int STAGE_BYTES = WMAIN + (ROPE ? WROPE : 0);
+  constexpr int STAGE_BYTES = WMAIN + (ROPE && !QK8 ? WROPE : 0);
   constexpr int RAW_CH = SAS_FP8_ROW_BYTES / 16;  // 16-byte chunks per fp8 row (41)
   constexpr int LATENT_BYTES = 512;      // fp8 row: e4m3 dims 0..511, then 4 fp32 scales, rope
   constexpr int RAW_DMA = TILE / NW;     // fp8: raw DMA instructions per wave and tile, a row each
   constexpr uint64_t RAW_LANES = (1ull << RAW_CH) - 1;  // the lanes of a row's DMA (0 .. 40)
   constexpr int RAW_STAGE = TILE * SAS_FP8_ROW_BYTES;   // 32 rows x 656 B
-  constexpr int NRAW = FP8 ? 3 : 0;      // raw ring depth
+  constexpr int NRAW = FP8 ? (QK8 ? 4 : 3) : 0;  // raw ring depth
   constexpr int LDS_BYTES = NSTG * STAGE_BYTES + NRAW * RAW_STAGE;
   static_assert(!FP8 || (DQK == 576 && __is_same(T, __bf16)), "fp8 rows: d_qk 576, bf16");
   static_assert(!(PAIR && FP8), "row pairs: native rows");
+  static_assert(!QK8 || FP8, "fp8 Q·Kᵀ reads fp8 rows");
   static_assert(RAW_CH <= 64 && RAW_CH * 16 == SAS_FP8_ROW_BYTES, "one fp8 row per DMA");
   constexpr int RPW = TILE / NW;         // main-part DMA instructions per wave and tile (4)
   constexpr int NROPE = ROPE ? TILE / 8 : 0;  // rope DMA instructions per tile (waves w < 4)
@@ -138,6 +144,10 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   __shared__ uint32_t tmask[RCH / TILE];
   __shared__ int first_neg[2];  // first -1 of the top-k scan (the slots alternate between scans)
   __shared__ int merge_word;    // split_arrive's answer to the workgroup
+  // QK8: the block scales of the tiles in the two bf16 stages, [stage][block][row]
+  // (36-float block stride: the four writers of a row hit four banks)
+  constexpr int K8_SSTRIDE = 36;
+  __shared__ float k8s[QK8 ? 2 : 1][4][K8_SSTRIDE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -292,6 +302,10 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
     // query fragment of the wave's 16 heads (B operand of Sᵀ = K·Qᵀ): k-step ks holds
     // dims 32 ks + 8 g4 .. + 7 of head `head`
     i16x8 qf[NKS];
+    // QK8: the e4m3 query of block blk (the 16x16x128 B operand: byte p of lane l is
+    // dim 128 blk + 32 (l / 16) + p of head l % 16) and its scale
+    i32x8 q8[QK8 ? 4 : 1];
+    float sq = 1.0f;
 
     // ---- scenario 3: position of the first -1 among the scanned top-k slots ----
     // (golden.py:48-53: the scan stops at the first -1). The first chunk's own
@@ -320,7 +334,13 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         const short* qrow =
             (const short*)a.q + ((size_t)(ok ? tok_w : 0) * a.num_heads + (ok ? head : 0)) * DQK;
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[ks] = *(const i16x8*)(qrow + 32 * ks + 8 * g4);
+        for (int ks = 0; ks < NKS; ++ks) {
+          // (QK8: latent k-step 4 blk + h holds dims 128 blk + 32 g4 + 8 h, the lane's
+          // quarter of e4m3 block blk)
+          const int dim = (QK8 && ks < NKS_MAIN) ? 128 * (ks >> 2) + 32 * g4 + 8 * (ks & 3)
+                                                 : 32 * ks + 8 * g4;
+          qf[ks] = *(const i16x8*)(qrow + dim);
+        }
       };
       // ---- resolve positions -> cache rows (bit 31: compressed cache) ----
       int cid[PER];
@@ -501,12 +521,12 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         return (lds_p)(kv_base + (uint32_t)((tile % NSTG) * STAGE_BYTES));
       };
       // ---- fp8 rows: raw DMA and dequantization ----
-      // Raw tile t goes to raw stage t % 3 as 32 rows of 656 bytes: this wave's
+      // Raw tile t goes to raw stage t % NRAW as 32 rows of 656 bytes: this wave's
       // instruction j copies row w + 8 j whole, lane i < 41 its 16-byte piece i,
       // from the row's address (lane j of raw_addrs, read into scalars) plus 16 i.
       // Past the chunk's last tile the rows are read from the zero row.
       auto raw_base = [&](int tile) -> uint32_t {
-        return kv_base + (uint32_t)(NSTG * STAGE_BYTES + (tile % 3) * RAW_STAGE);
+        return kv_base + (uint32_t)(NSTG * STAGE_BYTES + (tile % NRAW) * RAW_STAGE);
       };
       auto raw_addrs = [&](int tile) -> uint64_t {
         const bool real = tile < ntile;
@@ -516,7 +536,8 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       };
       auto raw_issue = [&](uint64_t ra, uint32_t voff, int tile, int j) {
         dma16_sbase_lanes(lane_row(ra, j), voff,
-                          raw_base(tile) + (uint32_t)((w + NW * j) * SAS_FP8_ROW_BYTES), RAW_LANES);
+                          raw_base(tile) + (uint32_t)((w + NW * j) * SAS_FP8_ROW_BYTES),
+                          RAW_LANES);
       };
       // Raw tile t (landed and published by a barrier) into bf16 stage t % 2 as
       // bf16(fp32(e4m3) * scale): wave w converts rows w + 8 k (k < 4), lane l dims
@@ -533,13 +554,17 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         const float sc8 = *(const float SAS_LDS*)(raw + LATENT_BYTES + 4 * (l >> 4));
         *(i16x8 SAS_LDS*)(st + (uint32_t)(wide_row_base(r) + 16 * l)) =
             fp8x8_dequant_bf16(make_uint2((uint32_t)v[0], (uint32_t)v[1]), sc8);
+        if constexpr (QK8) {
+          if ((l & 15) == 0) k8s[tile & 1][l >> 4][r] = sc8;  // block l / 16's scale of row r
+        }
       };
       auto convert_rope = [&](int tile) {
         const int x = 64 * w + lane_id_here();
         if (x < TILE * 8) {
           const int r = x >> 3, c = x & 7;
-          const i16x8 rp = *(const i16x8 SAS_LDS*)(raw_base(tile) + (uint32_t)(r * SAS_FP8_ROW_BYTES +
-                                                                    LATENT_BYTES + 16 + 16 * c));
+          const i16x8 rp = *(const i16x8 SAS_LDS*)(raw_base(tile) + (uint32_t)(r *
+                                                                   SAS_FP8_ROW_BYTES + LATENT_BYTES +
+                                                                   16 + 16 * c));
           *(i16x8 SAS_LDS*)(kv_base + (uint32_t)((tile % 2) * STAGE_BYTES + WMAIN +
                                                   16 * wide_rope_slot(wide_perm(r), c))) = rp;
         }
@@ -547,7 +572,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       auto convert = [&](int tile) {
 #pragma unroll
         for (int k = 0; k < TILE / NW; ++k) convert_row(tile, k);
-        convert_rope(tile);
+        if constexpr (!QK8) convert_rope(tile);
       };
 
       auto mma16 = [&](i16x8 x, i16x8 y, f32x4 c) -> f32x4 {
@@ -590,6 +615,83 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
           else s0 = mma16(op, qf[i >> 1], s0);
           hook(i);
           __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+
+      // ---- QK8: Q·Kᵀ of one tile from its raw rows. Lane l's A operands: row
+      // 16 rb + l % 16, bytes 128 blk + 32 (l / 16) .. + 31 of its e4m3 dims (block
+      // blk), and bf16 rope dims 512 + 32 kr + 8 (l / 16) .. + 7. Per 16-row block rb
+      // the scores are sq * sum_blk sk[blk][row] * d_blk + d_rope: the block dot
+      // products d_blk in fp32 (v_mfma_f32_16x16x128_f8f6f4), folded in block order
+      // with fused multiply-adds (block 0 a product), the rope part on two bf16
+      // k-steps. The MFMAs alternate between the two row blocks; a block's scale is
+      // folded in after the next MFMA is issued. ----
+      auto qk8_tile = [&](int tile, f32x4& s0, f32x4& s1, auto&& hook) {
+        const int l = lane_id_here();
+        const lds_p raw = (lds_p)(raw_base(tile) +
+                                  (uint32_t)((l & 15) * SAS_FP8_ROW_BYTES + 32 * (l >> 4)));
+        auto k8op = [&](int j) -> i32x8 {  // MFMA j: row block j & 1, e4m3 block j >> 1
+          const lds_p p = raw + (uint32_t)((j & 1) * 16 * SAS_FP8_ROW_BYTES + 128 * (j >> 1));
+          const i32x4 lo = *(const i32x4 SAS_LDS*)p;
+          const i32x4 hi = *(const i32x4 SAS_LDS*)(p + 16);
+          return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        auto kscale = [&](int j) -> f32x4 {  // scales of rows 16 rb + 4 (l / 16) + i
+          return *(const f32x4 SAS_LDS*)&k8s[tile & 1][j >> 1][16 * (j & 1) + 4 * (l >> 4)];
+        };
+        auto mma8 = [&](i32x8 x, i32x8 y) -> f32x4 {
+          // e4m3 x e4m3 (format selectors 0), no block scaling
+          return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              x, y, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+        };
+        f32x4 s8[2];
+        auto fold = [&](int j, f32x4 d, f32x4 sk) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            s8[j & 1][i] = (j < 2) ? d[i] * sk[i] : __builtin_fmaf(d[i], sk[i], s8[j & 1][i]);
+          // (here, not sunk to the end: a product kept for later holds its MFMA's
+          // four result registers across the tile)
+          asm volatile("" : "+v"(s8[j & 1]));
+        };
+        constexpr int N8 = 8;
+        i32x8 kb[2];
+        kb[0] = k8op(0);
+        kb[1] = k8op(1);
+        // (a block's product is folded two MFMAs after its own, when it has landed;
+        // its scales are read when it is issued)
+        f32x4 dq[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        f32x4 skq[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < N8; ++j) {
+          const i32x8 op = kb[j & 1];
+          if (j + 2 < N8) kb[j & 1] = k8op(j + 2);
+          const f32x4 d = mma8(op, q8[j >> 1]);
+          if (j > 1) fold(j - 2, dq[j & 1], skq[j & 1]);
+          dq[j & 1] = d;
+          skq[j & 1] = kscale(j);
+          hook(j);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // rope: k-steps 16 and 17 of each row block, from the raw rows' bf16 dims
+        f32x4 dr[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        // (row base + 32 (l / 16) + 528 - 16 (l / 16): the rope's chunk l / 16)
+        const lds_p rp = raw + (uint32_t)(LATENT_BYTES + 16 - 16 * (l >> 4));
+#pragma unroll
+        for (int kr = 0; kr < 2; ++kr)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            const i16x8 ko =
+                *(const i16x8 SAS_LDS*)(rp + (uint32_t)(rb * 16 * SAS_FP8_ROW_BYTES + 64 * kr));
+            dr[rb] = mma16(ko, qf[NKS_MAIN + kr], dr[rb]);
+            if (kr == 0) fold(N8 - 2 + rb, dq[rb], skq[rb]);
+            hook(N8 + 2 * kr + rb);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s0[i] = __builtin_fmaf(s8[0][i], sq, dr[0][i]);
+          s1[i] = __builtin_fmaf(s8[1][i], sq, dr[1][i]);
         }
       };
 
@@ -713,6 +815,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         // it also covers the DMAs issued before them)
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) asm volatile("" ::"v"(qf[ks]));
+        if constexpr (QK8) quantize_q(qf, q8, sq);
       }
       if constexpr (FP8) {
         wait_all_but(std::integral_constant<int, 2>{});  // this wave's raw DMAs of tile 0
@@ -737,7 +840,17 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         // (fp8 rows: tile t + 1 is dequantized into the bf16 stage tile t - 1 held,
         // a row at a time between the Q·Kᵀ MFMAs, whose matrix-core time the
         // conversion's VALU work runs beside)
-        qk_tile(sb, s0, s1, [&](int i) {
+        auto conv_hook = [&](int i) {
+          if constexpr (QK8) {
+            if (t + 1 < ntile) {
+#pragma unroll
+              for (int k = 0; k < TILE / NW; ++k)
+                if (i == 1 + 3 * k) convert_row(t + 1, k);
+            }
+          }
+        };
+        if constexpr (QK8) qk8_tile(t, s0, s1, conv_hook);
+        else qk_tile(sb, s0, s1, [&](int i) {
           if constexpr (FP8) {
             if (t + 1 < ntile) {
 #pragma unroll

@@ -59,8 +59,8 @@ def m_base_for(num_heads: int, item64: bool = False, batch: Optional[int] = None
     32 up to 32 heads and 64 up to 64 heads, as the reference. Above 64 heads an
     item holds all of a token's heads (128) when the call has at least
     ``WIDE_ITEM_MIN_BATCH`` sequences (``batch``; the 128-head kernel then serves
-    every head of the token from one gathered tile, native or fp8 rows), else 64;
-    ``item64`` (the fp8 Q·Kᵀ form, the pipelined kernel on native rows) keeps 64.
+    every head of the token from one gathered tile, native or fp8 rows, either Q·Kᵀ
+    form), else 64; ``item64`` (the pipelined kernel on native rows) keeps 64.
     The rule reads only values both schedulers and every entry point know alike
     (head count, kernel form, sequence count)."""
     if num_heads <= 32:
@@ -131,8 +131,8 @@ def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: in
                    fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK, item64: bool = False,
                    m_base: Optional[int] = None) -> torch.Tensor:
     """Run the C++ scheduler; returns an int32 CPU tensor of ``SAS_META_SIZE`` words.
-    ``item64``: the schedule is for a kernel form of 64-head items at most (the fp8
-    Q·Kᵀ form, the pipelined kernel; ``m_base_for``); ``m_base``: the item size
+    ``item64``: the schedule is for a kernel form of 64-head items at most (the
+    pipelined kernel; ``m_base_for``); ``m_base``: the item size
     (default ``m_base_for``)."""
     lib = _lib.load()
     b = len(act_q)
@@ -294,7 +294,8 @@ def sparse_attn_sharedkv_metadata(
     (or already on) that GPU, without reading them back; the words are the ones
     the host scheduler produces. ``kv_cache_dtype`` (no reference counterpart):
     ``"fp8_ds_mla"`` for calls on fp8 cache rows, and ``fp8_qk`` (no reference
-    counterpart) for calls of the fp8 Q·Kᵀ form, whose items hold at most 64 heads.
+    counterpart) for calls of the fp8 Q·Kᵀ form (checked against the row format;
+    both Q·Kᵀ forms take the same item sizes).
     Items hold 32, 64 or 128 heads (``m_base_for``: 128 only above 64 heads with at
     least ``WIDE_ITEM_MIN_BATCH`` sequences).
     """
@@ -316,7 +317,7 @@ def sparse_attn_sharedkv_metadata(
     core_num = min(int(aic_core_num), AIC_CORE_NUM)
     if fp8_qk and not _is_fp8(kv_cache_dtype):
         raise ValueError("fp8_qk needs kv_cache_dtype='fp8_ds_mla'")
-    item64 = bool(fp8_qk)
+    item64 = False  # (either Q·Kᵀ form of fp8 rows takes the same item sizes)
     if device is not None and torch.device(device).type == "cuda":
         # scheduled on that GPU from device-resident lengths: nothing is read back
         batch, act_q, uniform_q, act_kv = device_lengths(

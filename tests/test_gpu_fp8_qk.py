@@ -32,7 +32,7 @@ HAS_GPU = torch.cuda.is_available()
 requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
 
 if HAS_GPU:
-    from sparse_attn_sharedkv_amd import sparse_attn_sharedkv, sparse_flash_mla
+    from sparse_attn_sharedkv_amd import api, sparse_attn_sharedkv, sparse_flash_mla
 
 
 def _say(msg):
@@ -105,6 +105,40 @@ def test_fp8qk_topk_decode(heads, k, lens, sinks, cores):
     kw = _normal_fp8_case(lens=lens, heads=heads, k=k, seed=heads + k + cores, sinks=sinks)
     out, lse = _run(kw, core_num=cores)
     _check(out, lse, kw, vs_golden=True)
+
+
+def _run_items(kw, m_base, **extra):
+    """The call with items of ``m_base`` heads (128: the 128-head kernel, whose
+    Q·Kᵀ reads the e4m3 blocks straight from its raw ring)."""
+    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+    prep = api.prepare(**dev, fp8_qk=True, _m_base=m_base, **extra)
+    assert prep.args.m_base == m_base
+    api.launch(prep)
+    torch.cuda.synchronize()
+    out, lse = api.finalize(prep, True)
+    return out.cpu(), lse.cpu()
+
+
+@requires_gpu
+@pytest.mark.parametrize("heads,k,lens,sinks,cores", [
+    (128, 2048, [3000, 5000, 2100, 4097], False, 256),
+    (128, 2048, [1000, 2500], True, 256),        # thr < K: -1 padded rows
+    (128, 2048, [4000, 2999, 3500], True, 16),   # five pieces per item (merge kernel)
+    (128, 2048, [4000, 2999, 3500], True, 6),    # two pieces per item (merged in-kernel)
+    (96, 1030, [1100, 2000], True, 3),           # partial head block, split
+])
+def test_fp8qk_128_head_items(heads, k, lens, sinks, cores):
+    # 128-head items: against both oracles, and against the 64-head items' kernel
+    # (the same block dot products and folds, its own softmax steps)
+    _say(f"fp8 Q·Kᵀ, 128-head items H={heads} K={k} lens={lens} cores={cores}")
+    kw = _normal_fp8_case(lens=lens, heads=heads, k=k, seed=heads + k + cores + 1, sinks=sinks)
+    out, lse = _run_items(kw, 128, core_num=cores)
+    _check(out, lse, kw, vs_golden=True)
+    out64, lse64 = _run_items(kw, 64, core_num=cores)
+    d_out = (out.float() - out64.float()).abs().max().item()
+    d_lse = (lse - lse64).abs().max().item()
+    _say(f"128- vs 64-head items: out {d_out:.3g}, lse {d_lse:.3g}")
+    assert d_out <= 2e-2 and d_lse <= 1e-4
 
 
 @requires_gpu
