@@ -187,10 +187,10 @@ typedef struct SasAttnArgs {
    * which is small against golden for N(0,1)-scaled data but not for the reference
    * tests' U(-10, 10) data, so it is opt-in.
    * SAS_PHASE_ROW_ITEMS (bit 4, native rows) turns off row pairs: by default a launch
-   * whose sequences hold several query rows, with items of 64 heads (num_heads <= 64),
-   * no split items (num_fd == 0 and num_partial_slots == 0) and scenario 1 or 2, runs
-   * two consecutive query rows per workgroup on the 128-head kernel over the union of
-   * their attended rows (prefill: the two windows share all but two rows). No
+   * whose sequences hold several query rows, with items of 64 heads (num_heads <= 64)
+   * and scenario 1 or 2, runs two consecutive query rows per workgroup on the 128-head
+   * kernel over the union of their attended rows (prefill: the two windows share all
+   * but two rows); pieces of split items run alone. No
    * reference counterpart (the reference's prefill task is one query row,
    * kernel.py:262, :293); results agree with the one-row items to within rounding. */
   int32_t phases;

@@ -436,13 +436,12 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
 
 def uses_row_pairs(prep: Prepared) -> bool:
     """Whether the library runs this call as row pairs (two consecutive query rows
-    of 64 heads per workgroup on the 128-head kernel): the rule of the library's
-    launch (native rows, items of 64 heads with at most 64 heads, no split items,
-    scenarios 1 and 2, several query rows in some sequence)."""
+    of 64 heads per workgroup on the 128-head kernel; pieces of split items run
+    alone): the rule of the library's launch (native rows, items of 64 heads with
+    at most 64 heads, scenarios 1 and 2, several query rows in some sequence)."""
     a = prep.args
-    return (a.kv_format == _lib.KV_NATIVE and a.num_fd == 0 and a.num_partial_slots == 0
-            and a.m_base == 64 and a.num_heads <= 64 and a.scenario <= 2
-            and a.total_tokens > a.batch
+    return (a.kv_format == _lib.KV_NATIVE and a.m_base == 64 and a.num_heads <= 64
+            and a.scenario <= 2 and a.total_tokens > a.batch
             and not (prep.phase_bits & (_lib.SAS_PHASE_ROW_ITEMS | _lib.SAS_PHASE_PIPELINED)))
 
 

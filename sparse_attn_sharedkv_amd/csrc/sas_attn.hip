@@ -2437,14 +2437,14 @@ __global__ __launch_bounds__(MERGE_THREADS) void merge_kernel(const SasAttnArgs 
 }
 
 // Launches whose sequences hold several query rows run two consecutive rows of
-// 64 heads per workgroup on the 128-head kernel when no item is split (the host
-// schedule has no merge tasks and no partial slots) and each row attends a window
+// 64 heads per workgroup on the 128-head kernel when each row attends a window
 // and / or a dense compressed prefix: the two rows' lists then overlap in all but
-// a position or two, so one gathered tile serves both.
+// a position or two, so one gathered tile serves both (pieces of split items run
+// alone). The rule reads only what a host- and a device-built schedule's launch
+// both know, so both run the same kernel.
 static bool row_pairs_ok(const SasAttnArgs& a) {
-  return !(a.phases & SAS_PHASE_ROW_ITEMS) && a.kv_format == SAS_KV_NATIVE && a.num_fd == 0 &&
-         a.num_partial_slots == 0 && a.scenario <= 2 && a.num_heads <= 64 && a.m_base == 64 &&
-         a.total_tokens > a.batch;
+  return !(a.phases & SAS_PHASE_ROW_ITEMS) && a.kv_format == SAS_KV_NATIVE &&
+         a.scenario <= 2 && a.num_heads <= 64 && a.m_base == 64 && a.total_tokens > a.batch;
 }
 
 template <int DQK, int NHG, typename T, int KVF>

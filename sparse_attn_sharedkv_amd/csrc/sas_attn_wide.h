@@ -97,8 +97,8 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   // PAIR: items of 64 heads (at most 64 heads, one head block), two consecutive
   // query rows of a sequence at a time — waves 0..3 take row s, waves 4..7 row
   // s + 1, over the union of the two rows' positions, each wave masking the
-  // positions its own row does not attend. Only for schedules without split
-  // items, windows and dense compressed prefixes (scenarios 1, 2).
+  // positions its own row does not attend. Windows and dense compressed
+  // prefixes only (scenarios 1, 2); a piece of a split item runs alone.
   constexpr int IMB = PAIR ? 64 : MB;    // heads per item (m-block)
   constexpr int NT = 64 * NW;            // threads
   constexpr bool ROPE = DQK == 576;      // 64 extra rope dims after the 512 main dims
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
   int s2b = a.s2_base;
   int nfa = a.num_fa;
   if (a.num_fd == SAS_SCHED_DEVICE) {
-    if (!dev_sched_ok(a, MB)) {
+    if (!dev_sched_ok(a, IMB)) {
       if (blockIdx.x == 0) nan_fill<T>(a, tid, NT);
       return;
     }
@@ -889,7 +889,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
     __syncthreads();  // (an item without rows: the previous item's staged rows are read out)
     {
       unsigned char* stg = kv_lds;
-      const int nh = min(MB, a.num_heads - hb * MB);  // heads of this item
+      const int nh = min(IMB, a.num_heads - hb * IMB);  // heads of this item
       constexpr int SROW = DV * 2 + 16;  // staging row stride (bytes; 16-byte aligned rows)
       constexpr int CPR = DV * 2 / 16;   // 16-byte chunks per row
       int tid_e = tid, hl_e = srow, dv_e = 4 * g4;
@@ -923,7 +923,9 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
           if (g4 == 0 && head_ok && tok_ok_w)
             a.lse[(size_t)tok_w * a.num_heads + head] = (m_run + __log2f(l_run)) * LN2;
         }
-      } else if (!PAIR && slot >= 0 && slot < a.num_partial_slots && a.workspace) {
+      } else if (slot >= 0 && slot < a.num_partial_slots && a.workspace) {
+        // (row pairs: a piece of a split item is never paired, so its heads are
+        // waves 0..3's, staging rows 0 .. 63)
         // fp16 partials (acc / l, scaled): the head's whole row sits in its four
         // lanes, whose max picks the scale
         const bool empty = !(l_run > 0.0f);
@@ -953,40 +955,40 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         const float lse_piece = empty ? -INFINITY : (m_run + __log2f(l_run)) * LN2;
         if (merge_here) {
           // read by another workgroup in this launch: agent-coherent stores
-          const __amdgpu_buffer_rsrc_t rs = partial_rsrc(a, MB, DV);
-          const uint32_t base = (uint32_t)slot * MB * DV * 2;
+          const __amdgpu_buffer_rsrc_t rs = partial_rsrc(a, IMB, DV);
+          const uint32_t base = (uint32_t)slot * IMB * DV * 2;
           for (int c = tid_e; c < nh * CPR; c += NT) {
             const int h = c / CPR, c16 = c - h * CPR;
             partial_store16(rs, base + (uint32_t)(h * DV * 2 + c16 * 16),
                             *(const i32x4*)(stg + h * SROW + c16 * 16));
           }
           if (g4 == 0 && head_ok) {
-            const uint32_t lo = (uint32_t)a.num_partial_slots * MB * DV * 2;
-            partial_store4(rs, lo + ((uint32_t)slot * MB + hl_e) * 4, lse_piece);
-            partial_store4(rs, lo + ((uint32_t)(a.num_partial_slots + slot) * MB + hl_e) * 4,
+            const uint32_t lo = (uint32_t)a.num_partial_slots * IMB * DV * 2;
+            partial_store4(rs, lo + ((uint32_t)slot * IMB + hl_e) * 4, lse_piece);
+            partial_store4(rs, lo + ((uint32_t)(a.num_partial_slots + slot) * IMB + hl_e) * 4,
                            ps.inv);
           }
         } else {
-          char* wbase = (char*)a.workspace + (size_t)slot * MB * DV * 2;
+          char* wbase = (char*)a.workspace + (size_t)slot * IMB * DV * 2;
           for (int c = tid_e; c < nh * CPR; c += NT) {
             const int h = c / CPR, c16 = c - h * CPR;
             *(i16x8*)(wbase + (size_t)h * DV * 2 + c16 * 16) =
                 *(const i16x8*)(stg + h * SROW + c16 * 16);
           }
           if (g4 == 0 && head_ok) {
-            float* wl = partial_lse(a, MB, DV);
-            wl[(size_t)slot * MB + hl_e] = lse_piece;
-            wl[(size_t)(a.num_partial_slots + slot) * MB + hl_e] = ps.inv;
+            float* wl = partial_lse(a, IMB, DV);
+            wl[(size_t)slot * IMB + hl_e] = lse_piece;
+            wl[(size_t)(a.num_partial_slots + slot) * IMB + hl_e] = ps.inv;
           }
         }
       }
     }
-    if (!PAIR && partial && merge_here) {
+    if (partial && merge_here) {
       // the piece that completes the item merges it (bit-identical to merge_kernel)
       const int slot0 = (first_item && j_start > 0) ? slot - cont_k : slot;
       if (slot0 >= 0 && slot < a.num_partial_slots && slot0 < SAS_MERGE_SYNC_WORDS) {
         const int npc = split_arrive(a, slot0, slot, bhi - blo, bhi == nblk, nblk, &merge_word);
-        if (npc > 0) merge_item_here<DV, T, MB, NW>(a, tok, hb, slot0, npc);
+        if (npc > 0) merge_item_here<DV, T, IMB, NW>(a, tok, hb, slot0, npc);
       }
     }
     if (partial) ++slot;

@@ -1,17 +1,19 @@
 """Row pairs: two consecutive query rows of 64 heads per workgroup.
 
 Launches whose sequences hold several query rows (prefill, multi-token decode)
-with items of 64 heads, no split items and windows and / or dense compressed
-prefixes (scenarios 1 and 2) run two consecutive query rows per workgroup on
-the 128-head kernel, over the union of the two rows' attended positions, each
-row masking what it does not attend (test_sparse_attn_sharedkv.py:105-219 runs
-these shapes as prefill). Checked here:
+with items of 64 heads and windows and / or dense compressed prefixes
+(scenarios 1 and 2) run two consecutive query rows per workgroup on the
+128-head kernel, over the union of the two rows' attended positions, each row
+masking what it does not attend; pieces of split items run alone
+(test_sparse_attn_sharedkv.py:105-219 runs these shapes as prefill). Checked
+here:
 
 * gathered rows pinned exactly (q = 0, sinks -inf, one-hot V rows, as in
   ``test_gpu_index_exact``): windows -1 / 0 / 5 / 127, dense compressed rows at
   ratios 4 and 16, ragged TND rows and padded BSND rows, sequences whose early
   rows attend nothing (more query rows than cached rows), odd row counts (a row
-  left without a partner), 48 and 64 heads, d_qk 512 and 576, few workgroups;
+  left without a partner), 48 and 64 heads, d_qk 512 and 576, few workgroups,
+  split items (merged in-kernel and by the merge kernel);
 * random data against the oracle under the benchmark bound (``check_strict``),
   and against the same call with one query row per item
   (``SAS_PHASE_ROW_ITEMS``) to within rounding.
@@ -65,6 +67,8 @@ def _pairs_on(prep):
     (2, -1, 4, "TND", [40, 17], [300, 500], 64, 512, 256),   # compressed rows only
     (2, 7, 16, "TND", [33, 20], [900, 400], 64, 576, 256),
     (2, 63, 4, "BSND", [12, 12], [100, 60], 64, 512, 256),
+    (2, 127, 4, "TND", [4], [800], 64, 576, 3),      # split items (2 pieces: merged in-kernel)
+    (2, 127, 4, "TND", [6], [1000], 64, 512, 256),   # every item in 3 pieces (merge kernel)
 ])
 def test_row_pairs_rows_exact(scenario, win, ratio, layout, qlens, kvlens, heads, d, cores):
     _say(f"scenario {scenario} win {win} ratio {ratio} {layout} qlens {qlens} H={heads} d={d} "
