@@ -1,4 +1,6 @@
-// Attention kernel, wide form: items of 128 query heads (native bf16 / fp16 rows).
+// Attention kernel, wide form: 128 query-head columns per workgroup — items of
+// 128 heads (native bf16 / fp16 rows, or fp8 rows in either Q·Kᵀ form), or two
+// consecutive query rows of 64 heads (row pairs, native rows).
 //
 // Included by sas_attn.hip after the shared helpers (DMA issue, index loads,
 // zero row, partial scales, item geometry).
@@ -26,6 +28,8 @@
 // Ring of 4 stages and one barrier per tile: at the top of tile t every wave
 // has waited for its own DMAs of t; the barrier publishes t and frees the
 // stage of t - 1, into which the DMAs of t + 3 go between the P·V MFMAs of t.
+// fp8 rows: a raw ring of 656-byte rows (3 stages, 4 in the fp8 Q·Kᵀ form) feeds
+// two bf16 stages, each tile dequantized one tile ahead (see the kernel).
 #pragma once
 
 #ifndef SAS_WKPF

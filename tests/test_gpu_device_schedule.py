@@ -134,6 +134,24 @@ def test_attention_from_device_schedule_is_bitwise_the_host_one(name, batch):
 
 
 @requires_gpu
+@pytest.mark.parametrize("name,extra", [
+    ("mla_decode_b64_h128_k2048", {}),
+    ("mla_fp8_decode_t128_h128_k2048", {}),
+    ("mla_fp8_decode_t128_h128_k2048", {"fp8_qk": True}),
+])
+def test_128_head_items_from_device_schedule(name, extra):
+    # 128 sequences: items of all 128 heads on the 128-head kernel (native rows,
+    # fp8 rows, the fp8 Q·Kᵀ form), whole, in two pieces (merged in-kernel) and in
+    # many pieces (merge kernel)
+    _say(f"device vs host schedule {name} {extra}, 128 sequences")
+    kw = gen.build_workload(name, device="cuda", seed=13, batch=128, ctx_override=[4096] * 128)
+    for cores in (256, 128, 512):
+        o_h, l_h = _run(sparse_flash_mla, kw, schedule="host", core_num=cores, **extra)
+        o_d, l_d = _run(sparse_flash_mla, kw, schedule="device", core_num=cores, **extra)
+        assert torch.equal(o_d, o_h) and torch.equal(l_d, l_h), f"core_num={cores}"
+
+
+@requires_gpu
 @pytest.mark.parametrize("name", ["scfa_prefill_b2", "cfa_prefill_b2"])
 def test_ragged_tnd_from_device_schedule(name):
     # TND with ragged cu_seqlens_q: lengths and prefixes derived on the GPU
