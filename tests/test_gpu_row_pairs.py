@@ -16,7 +16,8 @@ here:
   split items (merged in-kernel and by the merge kernel);
 * random data against the oracle under the benchmark bound (``check_strict``),
   and against the same call with one query row per item
-  (``SAS_PHASE_ROW_ITEMS``) to within rounding.
+  (``SAS_PHASE_ROW_ITEMS``) to within rounding: bf16 and fp16, windows up to
+  1023 rows (a pair's positions in two resolution chunks).
 """
 
 import math
@@ -85,13 +86,13 @@ def test_row_pairs_rows_exact(scenario, win, ratio, layout, qlens, kvlens, heads
     _verify(kw, idx, t1, t2, scenario, ratio, 16, 16, out1, lse1)
 
 
-def _prefill_case(scenario, rows, heads, win, ratio, seed):
+def _prefill_case(scenario, rows, heads, win, ratio, seed, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     bs = 128
     nblk = (rows + bs - 1) // bs
-    ori = (torch.randn(nblk * 2, bs, 1, 512, generator=g) * 0.5).to(torch.bfloat16)
+    ori = (torch.randn(nblk * 2, bs, 1, 512, generator=g) * 0.5).to(dtype)
     table = torch.randperm(nblk * 2, generator=g)[:nblk].to(torch.int32).reshape(1, nblk)
-    kw = dict(q=(torch.randn(rows, heads, 512, generator=g) * 0.5).to(torch.bfloat16),
+    kw = dict(q=(torch.randn(rows, heads, 512, generator=g) * 0.5).to(dtype),
               ori_kv=ori, ori_block_table=table,
               seqused_kv=torch.tensor([rows], dtype=torch.int32),
               cu_seqlens_q=torch.tensor([0, rows], dtype=torch.int32),
@@ -100,18 +101,21 @@ def _prefill_case(scenario, rows, heads, win, ratio, seed):
     if scenario == 2:
         ncmp = max(rows // ratio, 1)
         cb = (ncmp + bs - 1) // bs
-        kw.update(cmp_kv=(torch.randn(cb, bs, 1, 512, generator=g) * 0.5).to(torch.bfloat16),
+        kw.update(cmp_kv=(torch.randn(cb, bs, 1, 512, generator=g) * 0.5).to(dtype),
                   cmp_block_table=torch.arange(cb, dtype=torch.int32).reshape(1, cb),
                   cmp_ratio=ratio)
     return kw
 
 
 @requires_gpu
-@pytest.mark.parametrize("scenario,rows,win,ratio", [
-    (1, 1000, 127, 1), (1, 333, 31, 1), (2, 1000, 127, 128), (2, 600, 63, 4)])
-def test_row_pairs_match_oracle_and_row_items(scenario, rows, win, ratio):
-    _say(f"prefill scenario {scenario}, {rows} rows, window {win}, ratio {ratio}")
-    kw = _prefill_case(scenario, rows, 64, win, ratio, seed=rows + win)
+@pytest.mark.parametrize("scenario,rows,win,ratio,dtype", [
+    (1, 1000, 127, 1, torch.bfloat16), (1, 333, 31, 1, torch.float16),
+    (2, 1000, 127, 128, torch.bfloat16), (2, 600, 63, 4, torch.bfloat16),
+    (1, 1100, 1023, 1, torch.bfloat16),  # a pair's window union spans two 1024-row chunks
+])
+def test_row_pairs_match_oracle_and_row_items(scenario, rows, win, ratio, dtype):
+    _say(f"prefill scenario {scenario}, {rows} rows, window {win}, ratio {ratio}, {dtype}")
+    kw = _prefill_case(scenario, rows, 64, win, ratio, seed=rows + win, dtype=dtype)
     prep, out, lse = _run(kw)
     assert _pairs_on(prep), "expected the row-pair path"
     ref, ref_lse = sparse_attn_oracle(**kw)
