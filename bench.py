@@ -11,9 +11,9 @@ the gathered rows between calls. Inputs are resident in HBM and the schedule
 is precomputed before the timed region.
 
 Other workloads (``--workload``): the MTP and fp8 long-context decode shapes
-(the fp8 one with bf16 queries on the dequantized rows by default, the faster
-form; ``--qk fp8`` runs its Q·Kᵀ on fp8 MFMA with e4m3 queries, as the
-configuration names it),
+(the fp8 one with its Q·Kᵀ on fp8 MFMA with e4m3 queries and bf16 P·V by
+default, as the configuration names it; ``--qk bf16`` runs bf16 queries on the
+dequantized rows instead),
 and the reference's own 8K prefill test shapes (``swa_prefill_t8192_h64``,
 ``cfa_prefill_t8192_h64``, ``scfa_prefill_t8192_h64``: H=64, d=512, block 128),
 whose ``roofline`` counts q, out and the distinct cache rows once (the rows are
@@ -65,8 +65,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--qk", choices=("auto", "bf16", "fp8"), default="auto",
                     help="Q·Kᵀ form over fp8 cache rows: fp8 MFMA with e4m3 queries (fp8) or "
-                         "bf16 MFMA on the dequantized rows (bf16); auto = bf16, the faster one "
-                         "(measured on MI355X at 128 sequences, H=128, top-k 2048)")
+                         "bf16 MFMA on the dequantized rows (bf16); auto = fp8, the form the "
+                         "long-context fp8 configuration names (1-2 %% faster than bf16 on MI355X "
+                         "at 128 sequences, H=128, top-k 2048)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the benchmark, run 5 plain device copies of MIB MiB (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -225,7 +226,7 @@ def main():
     counts = workload_counts(sets[0])
     flops, nbytes = flops_and_bytes(counts)
     fp8_rows = sets[0].get("kv_cache_dtype") is not None
-    fp8_qk = fp8_rows and args.qk == "fp8"
+    fp8_qk = fp8_rows and args.qk in ("auto", "fp8")
     if args.qk == "fp8" and not fp8_rows:
         print("--qk fp8 needs a workload with fp8 cache rows", file=sys.stderr)
         sys.exit(2)

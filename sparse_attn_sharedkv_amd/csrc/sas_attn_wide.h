@@ -530,7 +530,8 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
       // from the row's address (lane j of raw_addrs, read into scalars) plus 16 i.
       // Past the chunk's last tile the rows are read from the zero row.
       auto raw_base = [&](int tile) -> uint32_t {
-        return kv_base + (uint32_t)(NSTG * STAGE_BYTES + (tile % NRAW) * RAW_STAGE);
+        constexpr int NR = NRAW > 0 ? NRAW : 1;  // (native rows have no raw ring)
+        return kv_base + (uint32_t)(NSTG * STAGE_BYTES + (tile % NR) * RAW_STAGE);
       };
       auto raw_addrs = [&](int tile) -> uint64_t {
         const bool real = tile < ntile;
