@@ -66,7 +66,7 @@ def parse():
     ap.add_argument("--qk", choices=("auto", "bf16", "fp8"), default="auto",
                     help="Q·Kᵀ form over fp8 cache rows: fp8 MFMA with e4m3 queries (fp8) or "
                          "bf16 MFMA on the dequantized rows (bf16); auto = fp8, the form the "
-                         "long-context fp8 configuration names (1-2 %% faster than bf16 on MI355X "
+                         "long-context fp8 configuration names (level with bf16 or up to 2 %% faster on MI355X "
                          "at 128 sequences, H=128, top-k 2048)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the benchmark, run 5 plain device copies of MIB MiB (the known-size "
