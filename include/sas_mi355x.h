@@ -79,8 +79,9 @@ extern "C" {
 
 /* Host-side scheduler (no GPU needed). Fills meta_out[SAS_META_SIZE].
  * act_q[b]: query rows of batch b; act_kv[b]: raw KV length of batch b.
- * m_base: heads per item: 32 when num_heads <= 32, 64 up to 64 heads and for fp8 rows;
- * above 64 heads on native rows 64 or 128 (one item per token: the 128-head kernel).
+ * m_base: heads per item: 32 when num_heads <= 32, 64 up to 64 heads; above 64 heads
+ * 64 or 128 (one item per token: the 128-head kernel, native or fp8 rows; the
+ * pipelined kernel, SAS_PHASE_PIPELINED, takes 64 only).
  * num_cores: workgroups to balance over (<= SAS_AIC_CORE_NUM).
  * s2_base: positions per schedulable block (multiple of 32).
  * min_split_blocks: an item is split across workgroups only into pieces of at
