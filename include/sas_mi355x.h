@@ -173,9 +173,10 @@ typedef struct SasAttnArgs {
   /* kernels to enqueue: bit 0 attention, bit 1 split-KV merge; neither means both.
    * A caller may enqueue the two phases as separate calls (attention first).
    * SAS_PHASE_PIPELINED (bit 2) runs native rows through the attention kernel
-   * that fp8 rows use (two waves per SIMD, software-pipelined); by default native
-   * rows take the one-wave-per-SIMD kernel, which is faster on them. Results of the
-   * two kernels agree to within rounding, not bit for bit.
+   * that fp8 rows of 64-head items use (two waves per SIMD, software-pipelined); by
+   * default native rows take the one-wave-per-SIMD kernel (the 128-head kernel for
+   * 128-head items and row pairs), which is faster on them. Results of the kernels
+   * agree to within rounding, not bit for bit.
    * SAS_PHASE_FP8_QK (bit 3, fp8 rows only) forms Q·Kᵀ on fp8 MFMA
    * (v_mfma_f32_16x16x128_f8f6f4): each head's 512 latent query dims are quantized
    * to e4m3 with one fp32 scale: inv = 448 / amax (an IEEE fp32 division), codes =
@@ -212,6 +213,11 @@ typedef struct SasAttnArgs {
   uint64_t* merge_sync;
 } SasAttnArgs;
 
+/* SasAttnArgs.phases bits beyond the attention / merge selection (see phases) */
+#define SAS_PHASE_PIPELINED 4
+#define SAS_PHASE_FP8_QK 8
+#define SAS_PHASE_ROW_ITEMS 16
+
 #define SAS_MERGE_SYNC_WORDS (2 * SAS_AIC_CORE_NUM) /* uint64 counters: one per partial slot */
 
 /* Launch the attention kernel and, when num_fd > 0 and the merge is not done inside
@@ -228,9 +234,6 @@ int sas_attention_launch(const SasAttnArgs* args, void* stream);
  * (else SAS_E_CAPACITY, nothing launched). Calls no hipMalloc/hipFree. All calls on
  * one device share its scratch array: calls that may overlap on one device (other
  * streams, concurrent threads) race and must be serialised by the caller. */
-#define SAS_PHASE_PIPELINED 4
-#define SAS_PHASE_FP8_QK 8
-#define SAS_PHASE_ROW_ITEMS 16
 #define SAS_NOALLOC_SCRATCH_BYTES (72ull << 20)
 int sas_attention_launch_noalloc(const SasAttnArgs* args, void* stream);
 
