@@ -14,9 +14,9 @@ cases run that second path:
   two-slot top-k list per sequence over block-size-1 caches, every sequence of
   another length, so a length or offset read for the wrong sequence shows as a
   wrong row;
-* 128 sequences of 128 heads at d_qk = d_v = 512 (128-head items on the wide
-  kernel's d_qk-512 instance): gathered rows exactly, and window / top-k values
-  (bf16, fp16) against the oracle under the benchmark bound.
+* 128 sequences of 128 heads (128-head items on the wide kernel): gathered rows
+  exactly at d_qk = 512, and window / top-k values at d_qk 512 and 576, bf16 and
+  fp16, against the oracle under the benchmark bound.
 """
 
 import math
@@ -78,8 +78,8 @@ def test_many_sequences_rows_exact(batch, heads):
 
 
 # 128 sequences of a 128-head call take 128-head items (every head of a token
-# against one gathered tile) on the wide kernel; with d_qk = 512 that is its own
-# instance (no rope part in the ring). Gathered rows exactly, then values.
+# against one gathered tile) on the wide kernel; d_qk 512 (no rope part in the
+# ring) and fp16 rows are instances of their own. Gathered rows exactly, then values.
 @requires_gpu
 def test_128_head_items_d512_rows_exact():
     _say("rows exact, 128 sequences, H=128, d=512 (128-head items)")
@@ -91,31 +91,33 @@ def test_128_head_items_d512_rows_exact():
 
 
 @requires_gpu
+@pytest.mark.parametrize("d", [512, 576])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("scenario", [1, 3])
-def test_128_head_items_d512_against_oracle(scenario, dtype):
+def test_128_head_items_against_oracle(scenario, dtype, d):
     from sparse_attn_sharedkv_amd import api, sparse_attn_sharedkv, sparse_attn_sharedkv_metadata
     from oracle.gen import build_case
 
     b = 128
-    _say(f"128 sequences, H=128, d=512, scenario {scenario}, {dtype}")
+    _say(f"128 sequences, H=128, d={d}, scenario {scenario}, {dtype}")
     rng = np.random.default_rng(500 + scenario)
     kv = [int(x) for x in rng.integers(300, 1500, size=b)]
     cu = list(np.concatenate([[0], np.cumsum([1] * b)]).astype(int))
-    cfg = dict(scenario=scenario, layout_q="TND", B=b, S1=1, T1=b, N1=128, N2=1, D=512,
+    cfg = dict(scenario=scenario, layout_q="TND", B=b, S1=1, T1=b, N1=128, N2=1, D=d,
                K=96 if scenario == 3 else 0,
                block_num1=sum(-(-x // 64) for x in kv) + 2, block_num2=sum(max(1, -(-(x // 4) // 64)) for x in kv) + 1,
                block_size1=64, block_size2=64, cu_seqlens_q=cu, seqused_kv=kv,
-               softmax_scale=1.0 / math.sqrt(512), cmp_ratio=4, ori_win_left=127,
+               softmax_scale=1.0 / math.sqrt(d), cmp_ratio=4, ori_win_left=127,
                ori_win_right=0, ori_mask_mode=4, cmp_mask_mode=3)
     kw = build_case(cfg, dtype, seed=600 + scenario)
+    kw["head_dim_v"] = 512  # (d_qk 576: the first 512 columns are V)
     # values scaled to U(-0.5, 0.5): the benchmark bound applies to every element
     for key in ("q", "ori_kv", "cmp_kv"):
         if kw.get(key) is not None:
             kw[key] = (kw[key].float() * 0.05).to(dtype)
     cuq = torch.tensor(cu, dtype=torch.int32)
     md = sparse_attn_sharedkv_metadata(
-        num_heads_q=128, num_heads_kv=1, head_dim=512, cu_seqlens_q=cuq,
+        num_heads_q=128, num_heads_kv=1, head_dim=d, cu_seqlens_q=cuq,
         seqused_kv=kw["seqused_kv"], batch_size=b, max_seqlen_q=1, max_seqlen_kv=max(kv),
         cmp_topk=cfg["K"], cmp_ratio=4, ori_win_left=127, layout_q="TND",
         has_cmp_kv=scenario >= 2)

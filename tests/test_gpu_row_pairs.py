@@ -86,36 +86,38 @@ def test_row_pairs_rows_exact(scenario, win, ratio, layout, qlens, kvlens, heads
     _verify(kw, idx, t1, t2, scenario, ratio, 16, 16, out1, lse1)
 
 
-def _prefill_case(scenario, rows, heads, win, ratio, seed, dtype=torch.bfloat16):
+def _prefill_case(scenario, rows, heads, win, ratio, seed, dtype=torch.bfloat16, d=512):
     g = torch.Generator().manual_seed(seed)
     bs = 128
     nblk = (rows + bs - 1) // bs
-    ori = (torch.randn(nblk * 2, bs, 1, 512, generator=g) * 0.5).to(dtype)
+    ori = (torch.randn(nblk * 2, bs, 1, d, generator=g) * 0.5).to(dtype)
     table = torch.randperm(nblk * 2, generator=g)[:nblk].to(torch.int32).reshape(1, nblk)
-    kw = dict(q=(torch.randn(rows, heads, 512, generator=g) * 0.5).to(dtype),
+    kw = dict(q=(torch.randn(rows, heads, d, generator=g) * 0.5).to(dtype),
               ori_kv=ori, ori_block_table=table,
               seqused_kv=torch.tensor([rows], dtype=torch.int32),
               cu_seqlens_q=torch.tensor([0, rows], dtype=torch.int32),
-              sinks=torch.rand(heads, generator=g) * 2 - 1, softmax_scale=1 / math.sqrt(512),
+              sinks=torch.rand(heads, generator=g) * 2 - 1, softmax_scale=1 / math.sqrt(d),
               ori_win_left=win, layout_q="TND", head_dim_v=512)
     if scenario == 2:
         ncmp = max(rows // ratio, 1)
         cb = (ncmp + bs - 1) // bs
-        kw.update(cmp_kv=(torch.randn(cb, bs, 1, 512, generator=g) * 0.5).to(dtype),
+        kw.update(cmp_kv=(torch.randn(cb, bs, 1, d, generator=g) * 0.5).to(dtype),
                   cmp_block_table=torch.arange(cb, dtype=torch.int32).reshape(1, cb),
                   cmp_ratio=ratio)
     return kw
 
 
 @requires_gpu
-@pytest.mark.parametrize("scenario,rows,win,ratio,dtype", [
-    (1, 1000, 127, 1, torch.bfloat16), (1, 333, 31, 1, torch.float16),
-    (2, 1000, 127, 128, torch.bfloat16), (2, 600, 63, 4, torch.bfloat16),
-    (1, 1100, 1023, 1, torch.bfloat16),  # a pair's window union spans two 1024-row chunks
+@pytest.mark.parametrize("scenario,rows,win,ratio,dtype,d", [
+    (1, 1000, 127, 1, torch.bfloat16, 512), (1, 333, 31, 1, torch.float16, 512),
+    (2, 1000, 127, 128, torch.bfloat16, 512), (2, 600, 63, 4, torch.bfloat16, 512),
+    (1, 1100, 1023, 1, torch.bfloat16, 512),  # a pair's window union spans two 1024-row chunks
+    (2, 500, 63, 4, torch.float16, 576),      # the d_qk-576 instances (rope part in the ring)
+    (1, 400, 127, 1, torch.bfloat16, 576),
 ])
-def test_row_pairs_match_oracle_and_row_items(scenario, rows, win, ratio, dtype):
-    _say(f"prefill scenario {scenario}, {rows} rows, window {win}, ratio {ratio}, {dtype}")
-    kw = _prefill_case(scenario, rows, 64, win, ratio, seed=rows + win, dtype=dtype)
+def test_row_pairs_match_oracle_and_row_items(scenario, rows, win, ratio, dtype, d):
+    _say(f"prefill scenario {scenario}, {rows} rows, window {win}, ratio {ratio}, {dtype}, d {d}")
+    kw = _prefill_case(scenario, rows, 64, win, ratio, seed=rows + win, dtype=dtype, d=d)
     prep, out, lse = _run(kw)
     assert _pairs_on(prep), "expected the row-pair path"
     ref, ref_lse = sparse_attn_oracle(**kw)
