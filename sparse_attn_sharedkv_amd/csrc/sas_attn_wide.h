@@ -842,6 +842,10 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         else wait_all_but(std::integral_constant<int, 2>{});  // this wave's share of tile t
         __syncthreads();                                       // barrier t
         f32x4 s0, s1;
+        // Q·Kᵀ and the softmax at wave priority 1, P·V at 0: of the SIMD's two
+        // waves, one still in the first half of its tile wins issue over one
+        // already in P·V, so the slower wave reaches the next barrier sooner
+        __builtin_amdgcn_s_setprio(1);
         // (fp8 rows: tile t + 1 is dequantized into the bf16 stage tile t - 1 held,
         // a row at a time between the Q·Kᵀ MFMAs, whose matrix-core time the
         // conversion's VALU work runs beside)
@@ -867,6 +871,7 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
         });
         float alpha;
         const i16x8 pk = softmax_tile(t, s0, s1, alpha);
+        __builtin_amdgcn_s_setprio(0);
         if constexpr (FP8) {
           DmaAddrs dd;
           dd.main = raw_addrs(t + 3);
