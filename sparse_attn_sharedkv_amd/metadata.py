@@ -51,21 +51,30 @@ DEFAULT_FD_HEAD_CHUNK = 64    # heads per merge task (a whole 64-head item)
 # sequences, 62.9 us per call with 64-head items against 67.0 us; 128-head items
 # are ahead from 128 query rows on).
 WIDE_ITEM_MIN_BATCH = 128
+# fp8 rows take 128-head items from this many sequences on: their 64-head items
+# run on the pipelined kernel, which the 128-head kernel beats from 32 sequences
+# (measured on MI355X, top-k 2048 decode, H = 128, bf16 / fp8 Q·Kᵀ form: 32
+# sequences 49.6 / 51.2 us per call against 50.8 / 59.7; 64 sequences 71.3 /
+# 72.2 against 79.8 / 91.6; at 16 sequences 40.6 / 42.3 against 36.2 / 43.6).
+WIDE_ITEM_MIN_BATCH_FP8 = 32
 
 
-def m_base_for(num_heads: int, item64: bool = False, batch: Optional[int] = None) -> int:
+def m_base_for(num_heads: int, item64: bool = False, batch: Optional[int] = None,
+               fp8_rows: bool = False) -> int:
     """Heads per schedulable item (the reference's mBaseSize, metadata.py:388).
 
     32 up to 32 heads and 64 up to 64 heads, as the reference. Above 64 heads an
     item holds all of a token's heads (128) when the call has at least
-    ``WIDE_ITEM_MIN_BATCH`` sequences (``batch``; the 128-head kernel then serves
-    every head of the token from one gathered tile, native or fp8 rows, either Q·Kᵀ
-    form), else 64; ``item64`` (the pipelined kernel on native rows) keeps 64.
-    The rule reads only values both schedulers and every entry point know alike
-    (head count, kernel form, sequence count)."""
+    ``WIDE_ITEM_MIN_BATCH`` sequences (``batch``), or ``WIDE_ITEM_MIN_BATCH_FP8``
+    on fp8 cache rows (``fp8_rows``; either Q·Kᵀ form): the 128-head kernel then
+    serves every head of the token from one gathered tile; else 64. ``item64``
+    (the pipelined kernel on native rows) keeps 64. The rule reads only values
+    both schedulers and every entry point know alike (head count, cache row
+    format, kernel form, sequence count)."""
     if num_heads <= 32:
         return 32
-    if num_heads <= 64 or item64 or batch is None or batch < WIDE_ITEM_MIN_BATCH:
+    need = WIDE_ITEM_MIN_BATCH_FP8 if fp8_rows else WIDE_ITEM_MIN_BATCH
+    if num_heads <= 64 or item64 or batch is None or batch < need:
         return 64
     return 128
 
@@ -129,15 +138,15 @@ def build_metadata(*, act_q: Sequence[int], act_kv: Sequence[int], num_heads: in
                    core_num: int = DEFAULT_CORE_NUM, s2_base: int = DEFAULT_S2_BASE,
                    min_split_blocks: int = DEFAULT_MIN_SPLIT_BLOCKS,
                    fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK, item64: bool = False,
-                   m_base: Optional[int] = None) -> torch.Tensor:
+                   m_base: Optional[int] = None, fp8_rows: bool = False) -> torch.Tensor:
     """Run the C++ scheduler; returns an int32 CPU tensor of ``SAS_META_SIZE`` words.
     ``item64``: the schedule is for a kernel form of 64-head items at most (the
     pipelined kernel; ``m_base_for``); ``m_base``: the item size
-    (default ``m_base_for``)."""
+    (default ``m_base_for``, with ``fp8_rows`` for calls on fp8 cache rows)."""
     lib = _lib.load()
     b = len(act_q)
     if m_base is None:
-        m_base = m_base_for(int(num_heads), item64, b)
+        m_base = m_base_for(int(num_heads), item64, b, fp8_rows)
     out = torch.zeros(SAS_META_SIZE, dtype=torch.int32)
     aq = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_q])
     ak = (ctypes.c_int32 * max(b, 1))(*[int(x) for x in act_kv])
@@ -197,7 +206,7 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
                           fd_head_chunk: int = DEFAULT_FD_HEAD_CHUNK,
                           stream: Optional[torch.cuda.Stream] = None,
                           out: Optional[torch.Tensor] = None, item64: bool = False,
-                          m_base: Optional[int] = None) -> torch.Tensor:
+                          m_base: Optional[int] = None, fp8_rows: bool = False) -> torch.Tensor:
     """Run the on-device scheduler (``sas_metadata_build_device``) on the current stream.
 
     ``act_q`` / ``act_kv``: int32 ``[batch]`` tensors on the GPU (``act_q`` None: every
@@ -229,7 +238,7 @@ def build_metadata_device(*, batch: int, act_q: Optional[torch.Tensor], act_kv: 
         raise ValueError(f"out must be a contiguous int32 [{SAS_META_SIZE}] tensor on {dev}")
     st = stream if stream is not None else torch.cuda.current_stream(dev)
     if m_base is None:
-        m_base = m_base_for(int(num_heads), item64, int(batch))
+        m_base = m_base_for(int(num_heads), item64, int(batch), fp8_rows)
     rc = lib.sas_metadata_build_device(
         ctypes.c_void_p(out.data_ptr()), int(batch),
         ctypes.c_void_p(act_q.data_ptr() if act_q is not None else 0), int(uniform_q),
@@ -297,7 +306,8 @@ def sparse_attn_sharedkv_metadata(
     counterpart) for calls of the fp8 Q·Kᵀ form (checked against the row format;
     both Q·Kᵀ forms take the same item sizes).
     Items hold 32, 64 or 128 heads (``m_base_for``: 128 only above 64 heads with at
-    least ``WIDE_ITEM_MIN_BATCH`` sequences).
+    least ``WIDE_ITEM_MIN_BATCH`` sequences, ``WIDE_ITEM_MIN_BATCH_FP8`` on fp8
+    rows), so a schedule for fp8 rows must be built with ``kv_cache_dtype``.
     """
     del cu_seqlens_cmp_kv, head_dim, ori_topk, aiv_core_num
     if num_heads_kv != 1:
@@ -318,6 +328,7 @@ def sparse_attn_sharedkv_metadata(
     if fp8_qk and not _is_fp8(kv_cache_dtype):
         raise ValueError("fp8_qk needs kv_cache_dtype='fp8_ds_mla'")
     item64 = False  # (either Q·Kᵀ form of fp8 rows takes the same item sizes)
+    fp8_rows = _is_fp8(kv_cache_dtype)
     if device is not None and torch.device(device).type == "cuda":
         # scheduled on that GPU from device-resident lengths: nothing is read back
         batch, act_q, uniform_q, act_kv = device_lengths(
@@ -328,7 +339,7 @@ def sparse_attn_sharedkv_metadata(
                                      act_kv=act_kv, num_heads=num_heads_q,
                                      ori_win_left=ori_win_left, scenario=scenario,
                                      cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
-                                     core_num=core_num, item64=item64)
+                                     core_num=core_num, item64=item64, fp8_rows=fp8_rows)
     act_q, act_kv = resolve_lengths(layout_q=layout_q, layout_kv=layout_kv,
                                     cu_seqlens_q=cu_seqlens_q,
                                     cu_seqlens_ori_kv=cu_seqlens_ori_kv, seqused_q=seqused_q,
@@ -337,5 +348,5 @@ def sparse_attn_sharedkv_metadata(
     md = build_metadata(act_q=act_q, act_kv=act_kv, num_heads=num_heads_q,
                         ori_win_left=ori_win_left, scenario=scenario,
                         cmp_ratio=max(int(cmp_ratio), 1), cmp_topk=int(cmp_topk),
-                        core_num=core_num, item64=item64)
+                        core_num=core_num, item64=item64, fp8_rows=fp8_rows)
     return md.to(device) if device is not None else md

@@ -32,8 +32,8 @@ HAS_GPU = torch.cuda.is_available()
 requires_gpu = pytest.mark.skipif(not HAS_GPU, reason="needs a ROCm GPU")
 
 if HAS_GPU:
-    from sparse_attn_sharedkv_amd import (sparse_attn_sharedkv, sparse_attn_sharedkv_metadata,
-                                          sparse_flash_mla)
+    from sparse_attn_sharedkv_amd import (api, sparse_attn_sharedkv,
+                                          sparse_attn_sharedkv_metadata, sparse_flash_mla)
     from sparse_attn_sharedkv_amd.metadata import build_metadata, build_metadata_device
 
 
@@ -134,17 +134,22 @@ def test_attention_from_device_schedule_is_bitwise_the_host_one(name, batch):
 
 
 @requires_gpu
-@pytest.mark.parametrize("name,extra", [
-    ("mla_decode_b64_h128_k2048", {}),
-    ("mla_fp8_decode_t128_h128_k2048", {}),
-    ("mla_fp8_decode_t128_h128_k2048", {"fp8_qk": True}),
+@pytest.mark.parametrize("name,extra,batch", [
+    ("mla_decode_b64_h128_k2048", {}, 128),
+    ("mla_fp8_decode_t128_h128_k2048", {}, 128),
+    ("mla_fp8_decode_t128_h128_k2048", {"fp8_qk": True}, 128),
+    ("mla_fp8_decode_t128_h128_k2048", {}, 32),  # fp8 rows: 128-head items from 32 on
+    ("mla_fp8_decode_t128_h128_k2048", {"fp8_qk": True}, 48),
 ])
-def test_128_head_items_from_device_schedule(name, extra):
-    # 128 sequences: items of all 128 heads on the 128-head kernel (native rows,
-    # fp8 rows, the fp8 Q·Kᵀ form), whole, in two pieces (merged in-kernel) and in
-    # many pieces (merge kernel)
-    _say(f"device vs host schedule {name} {extra}, 128 sequences")
-    kw = gen.build_workload(name, device="cuda", seed=13, batch=128, ctx_override=[4096] * 128)
+def test_128_head_items_from_device_schedule(name, extra, batch):
+    # items of all 128 heads on the 128-head kernel (native rows from 128
+    # sequences, fp8 rows and the fp8 Q·Kᵀ form from 32), whole, in two pieces
+    # (merged in-kernel) and in many pieces (merge kernel)
+    _say(f"device vs host schedule {name} {extra}, {batch} sequences")
+    kw = gen.build_workload(name, device="cuda", seed=13, batch=batch,
+                            ctx_override=[4096] * batch)
+    prep = api.prepare(**kw, **extra)
+    assert prep.args.m_base == 128, prep.args.m_base
     for cores in (256, 128, 512):
         o_h, l_h = _run(sparse_flash_mla, kw, schedule="host", core_num=cores, **extra)
         o_d, l_d = _run(sparse_flash_mla, kw, schedule="device", core_num=cores, **extra)

@@ -162,6 +162,21 @@ def test_fp8_attention_matches_oracle(heads, k, lens, sinks):
     _check(out, lse, kw)
 
 
+@requires_gpu
+@pytest.mark.parametrize("batch", [32, 40])
+def test_fp8_128_head_items_from_32_sequences(batch):
+    # fp8 rows take 128-head items from 32 sequences on (m_base_for): the default
+    # path of such a call runs the 128-head kernel, checked against the oracle
+    _say(f"fp8 rows, {batch} sequences, H=128: 128-head items by default")
+    rng = np.random.default_rng(batch)
+    lens = [int(x) for x in rng.integers(600, 2600, size=batch)]
+    kw = _fp8_case(lens=lens, heads=128, k=512, seed=batch, sinks="uniform")
+    prep = api.prepare(**{k: v for k, v in _dev(kw).items() if k != "topk_cmp"})
+    assert prep.args.m_base == 128, prep.args.m_base
+    out, lse = _run(kw)
+    _check(out, lse, kw)
+
+
 def _run_pipelined(kw, **extra):
     """Native rows through the kernel fp8 rows use (SAS_PHASE_PIPELINED)."""
     kw = {k: v for k, v in _dev(kw).items() if k != "topk_cmp"}

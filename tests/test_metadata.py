@@ -211,3 +211,26 @@ def test_invalid_arguments_raise():
         sparse_attn_sharedkv_metadata(num_heads_q=64, num_heads_kv=2, head_dim=512,
                                       seqused_kv=torch.tensor([10]), batch_size=1,
                                       max_seqlen_q=1)
+
+
+def test_item_size_rule_for_fp8_rows():
+    # above 64 heads: 128-head items from 128 sequences on native rows, from 32 on
+    # fp8 rows (either Q·Kᵀ form); the pipelined form and <= 64 heads keep theirs
+    assert M.m_base_for(128, batch=127) == 64 and M.m_base_for(128, batch=128) == 128
+    assert M.m_base_for(128, batch=31, fp8_rows=True) == 64
+    assert M.m_base_for(128, batch=32, fp8_rows=True) == 128
+    assert M.m_base_for(96, batch=40, fp8_rows=True) == 128
+    assert M.m_base_for(64, batch=512, fp8_rows=True) == 64
+    assert M.m_base_for(32, batch=512, fp8_rows=True) == 32
+    assert M.m_base_for(128, item64=True, batch=512, fp8_rows=True) == 64
+    # the public entry point picks the size from the cache row format it is given
+    lens = [3000] * 40
+    common = dict(num_heads_q=128, num_heads_kv=1, head_dim=576,
+                  seqused_kv=torch.tensor(lens, dtype=torch.int32), batch_size=40,
+                  max_seqlen_q=1, max_seqlen_kv=3000, cmp_topk=2048, cmp_ratio=1,
+                  ori_win_left=-1, layout_q="BSND", has_cmp_kv=True)
+    assert config_row(sparse_attn_sharedkv_metadata(**common))["m_base"] == 64
+    md8 = sparse_attn_sharedkv_metadata(**common, kv_cache_dtype="fp8_ds_mla")
+    assert config_row(md8)["m_base"] == 128
+    md8q = sparse_attn_sharedkv_metadata(**common, kv_cache_dtype="fp8_ds_mla", fp8_qk=True)
+    assert torch.equal(md8q, md8)
