@@ -45,12 +45,13 @@ DEFAULT_FD_HEAD_CHUNK = 64    # heads per merge task (a whole 64-head item)
 
 
 # Above 64 heads, native rows take items of every head of a token (128) from this
-# many sequences on: with fewer, 128-head items need more pieces per item to fill
-# the 256 workgroups, and their split-KV partials cost more than reading each
-# gathered row once per 64 heads (measured on MI355X: top-k 2048 decode at 64
-# sequences, 62.9 us per call with 64-head items against 67.0 us; 128-head items
-# are ahead from 128 query rows on).
-WIDE_ITEM_MIN_BATCH = 128
+# many sequences on. Up to 64 sequences 64-head items fill the 256 workgroups in at
+# most two pieces per item, merged inside the attention kernel; from 65 on they
+# need three, and 128-head items are ahead (measured on MI355X, top-k 2048 decode,
+# H = 128, us per call with 64- / 128-head items: 32 sequences 42.7 / 48.4, 64
+# sequences 65.1 / 66.8, 65 sequences 88.2 / 72.2, 96 sequences 112.9 / 93.0,
+# 112 sequences 104.7 / 98.2).
+WIDE_ITEM_MIN_BATCH = 65
 # fp8 rows take 128-head items from this many sequences on: their 64-head items
 # run on the pipelined kernel, which the 128-head kernel beats from 32 sequences
 # (measured on MI355X, top-k 2048 decode, H = 128, bf16 / fp8 Q·Kᵀ form: 32

@@ -136,13 +136,14 @@ def test_attention_from_device_schedule_is_bitwise_the_host_one(name, batch):
 @requires_gpu
 @pytest.mark.parametrize("name,extra,batch", [
     ("mla_decode_b64_h128_k2048", {}, 128),
+    ("mla_decode_b64_h128_k2048", {}, 72),  # native rows: 128-head items from 65 on
     ("mla_fp8_decode_t128_h128_k2048", {}, 128),
     ("mla_fp8_decode_t128_h128_k2048", {"fp8_qk": True}, 128),
     ("mla_fp8_decode_t128_h128_k2048", {}, 32),  # fp8 rows: 128-head items from 32 on
     ("mla_fp8_decode_t128_h128_k2048", {"fp8_qk": True}, 48),
 ])
 def test_128_head_items_from_device_schedule(name, extra, batch):
-    # items of all 128 heads on the 128-head kernel (native rows from 128
+    # items of all 128 heads on the 128-head kernel (native rows from 65
     # sequences, fp8 rows and the fp8 Q·Kᵀ form from 32), whole, in two pieces
     # (merged in-kernel) and in many pieces (merge kernel)
     _say(f"device vs host schedule {name} {extra}, {batch} sequences")

@@ -214,9 +214,9 @@ def test_invalid_arguments_raise():
 
 
 def test_item_size_rule_for_fp8_rows():
-    # above 64 heads: 128-head items from 128 sequences on native rows, from 32 on
+    # above 64 heads: 128-head items from 65 sequences on native rows, from 32 on
     # fp8 rows (either Q·Kᵀ form); the pipelined form and <= 64 heads keep theirs
-    assert M.m_base_for(128, batch=127) == 64 and M.m_base_for(128, batch=128) == 128
+    assert M.m_base_for(128, batch=64) == 64 and M.m_base_for(128, batch=65) == 128
     assert M.m_base_for(128, batch=31, fp8_rows=True) == 64
     assert M.m_base_for(128, batch=32, fp8_rows=True) == 128
     assert M.m_base_for(96, batch=40, fp8_rows=True) == 128
