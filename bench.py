@@ -150,11 +150,13 @@ def profiled_counters(workload, kernel):
     return out
 
 
-def cpu_baseline(inputs, counts, max_tokens=64, fp8_qk=False):
+def cpu_baseline(inputs, counts, max_tokens=64, fp8_qk=False, budget_s=20.0):
     """Golden-faithful CPU restatement (oracle/) over the query rows of one input set.
 
     Times up to ``max_tokens`` rows (all of them for the benchmark workloads up to
-    64 tokens) and scales the rate to the whole call (FLOPs of the rows timed).
+    64 tokens; fewer when one row takes long enough that three passes would
+    exceed about ``budget_s`` seconds) and scales the rate to the whole call
+    (FLOPs of the rows timed).
     """
     import torch
 
@@ -172,26 +174,38 @@ def cpu_baseline(inputs, counts, max_tokens=64, fp8_qk=False):
     idx = kw["cmp_sparse_indices"]
     idx_flat = None if idx is None else idx.reshape(q_flat.shape[0], -1)
     every = [(b, s) for b in range(nb) for s in range(act_q[b])]
-    step = max(1, len(every) // max_tokens)  # evenly spaced sample (prefill rows differ in length)
-    rows = every[::step][:max_tokens]
+
+    def one_row(b, s):
+        t = prefix[b] + s
+        ori, cmp = token_rows(
+            b=b, s=s, act_q=act_q[b], act_kv=lens[b], ori_kv=kw["ori_kv"],
+            ori_block_table=kw["ori_block_table"], cmp_kv=kw["cmp_kv"],
+            cmp_block_table=kw["cmp_block_table"],
+            cmp_idx_row=None if idx_flat is None else idx_flat[t].tolist(),
+            cmp_ratio=kw["cmp_ratio"], ori_win_left=kw["ori_win_left"],
+            kv_cache_dtype=kw.get("kv_cache_dtype"), raw=fp8_qk)
+        (attend_token_fp8qk if fp8_qk else attend_token)(
+            q_flat[t], [ori, cmp], kw["sinks"], kw["softmax_scale"], d_v=kw["head_dim_v"])
+        return ori.shape[0] + cmp.shape[0]
+
+    # bound the sample: one untimed row sizes it to about budget_s for three passes
+    t0 = time.perf_counter()
+    one_row(*every[len(every) // 2])
+    per_row = time.perf_counter() - t0
+    n = max(2, min(max_tokens, int(budget_s / (3 * max(per_row, 1e-6)))))
+    step = max(1, len(every) // n)  # evenly spaced sample (prefill rows differ in length)
+    rows = every[::step][:n]
     times = []
     attended = 0
     for rep in range(3):
         t0 = time.perf_counter()
         for b, s in rows:
-            t = prefix[b] + s
-            ori, cmp = token_rows(
-                b=b, s=s, act_q=act_q[b], act_kv=lens[b], ori_kv=kw["ori_kv"],
-                ori_block_table=kw["ori_block_table"], cmp_kv=kw["cmp_kv"],
-                cmp_block_table=kw["cmp_block_table"],
-                cmp_idx_row=None if idx_flat is None else idx_flat[t].tolist(),
-                cmp_ratio=kw["cmp_ratio"], ori_win_left=kw["ori_win_left"],
-                kv_cache_dtype=kw.get("kv_cache_dtype"), raw=fp8_qk)
-            (attend_token_fp8qk if fp8_qk else attend_token)(
-                q_flat[t], [ori, cmp], kw["sinks"], kw["softmax_scale"], d_v=kw["head_dim_v"])
+            got = one_row(b, s)
             if rep == 0:
-                attended += ori.shape[0] + cmp.shape[0]
+                attended += got
         times.append(time.perf_counter() - t0)
+        print(f"[bench] cpu baseline pass {rep + 1}/3: {len(rows)} rows, {times[-1]:.1f} s",
+              file=sys.stderr, flush=True)
     sec = sorted(times)[1]
     flops, _ = flops_and_bytes(counts)
     share = attended / max(counts["rows"], 1)  # FLOP share of the sampled rows
