@@ -273,7 +273,11 @@ def prepare(q: torch.Tensor, *, ori_kv: torch.Tensor, cmp_kv: Optional[torch.Ten
     fp8_rows = kv_fmt == _lib.KV_FP8_DS_MLA
     # items of at most 64 heads: the fp8 Q·Kᵀ form and the pipelined kernel (m_base_for)
     item64 = _pipelined
-    m_base = m_base_for(int(n1), item64, nb, fp8_rows) if _m_base is None else int(_m_base)
+    # the item size: by query rows for a schedule this call builds, by sequences
+    # for one it is handed (the count its builder used, m_base_for)
+    m_base = (m_base_for(int(n1), item64, nb, fp8_rows,
+                         rows=int(total) if metadata is None else None)
+              if _m_base is None else int(_m_base))
     if not m_base_valid(int(n1), item64, m_base):
         raise ValueError(f"no kernel for items of {m_base} heads at {n1} heads")
     row_width = _lib.FP8_ROW_BYTES if fp8_rows else d

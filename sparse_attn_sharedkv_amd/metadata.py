@@ -61,7 +61,7 @@ WIDE_ITEM_MIN_BATCH_FP8 = 32
 
 
 def m_base_for(num_heads: int, item64: bool = False, batch: Optional[int] = None,
-               fp8_rows: bool = False) -> int:
+               fp8_rows: bool = False, rows: Optional[int] = None) -> int:
     """Heads per schedulable item (the reference's mBaseSize, metadata.py:388).
 
     32 up to 32 heads and 64 up to 64 heads, as the reference. Above 64 heads an
@@ -69,13 +69,19 @@ def m_base_for(num_heads: int, item64: bool = False, batch: Optional[int] = None
     ``WIDE_ITEM_MIN_BATCH`` sequences (``batch``), or ``WIDE_ITEM_MIN_BATCH_FP8``
     on fp8 cache rows (``fp8_rows``; either Q·Kᵀ form): the 128-head kernel then
     serves every head of the token from one gathered tile; else 64. ``item64``
-    (the pipelined kernel on native rows) keeps 64. The rule reads only values
-    both schedulers and every entry point know alike (head count, cache row
-    format, kernel form, sequence count)."""
+    (the pipelined kernel on native rows) keeps 64.
+
+    ``rows`` (the call's query rows) replaces the sequence count where the caller
+    builds the schedule for its own launch (a call without ``metadata``): calls of
+    several rows per sequence then take 128-head items too (MTP, 128-head
+    prefill). Schedules handed from one entry point to another count sequences,
+    the one value every entry point and both schedulers know alike (a schedule
+    built on the GPU from a ragged TND call holds its row count only there)."""
     if num_heads <= 32:
         return 32
     need = WIDE_ITEM_MIN_BATCH_FP8 if fp8_rows else WIDE_ITEM_MIN_BATCH
-    if num_heads <= 64 or item64 or batch is None or batch < need:
+    n = rows if rows is not None else batch
+    if num_heads <= 64 or item64 or n is None or n < need:
         return 64
     return 128
 

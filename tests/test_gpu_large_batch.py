@@ -130,3 +130,41 @@ def test_128_head_items_against_oracle(scenario, dtype, d):
     ref, ref_lse = sparse_attn_oracle(**okw)
     err = check_strict(out.cpu(), ref, lse.cpu(), ref_lse)
     _say(f"scenario {scenario} {dtype}: max |out - oracle| {err['out_max_abs']:.3g}")
+
+
+@requires_gpu
+@pytest.mark.parametrize("scenario", [1, 3])
+def test_multi_row_128_heads_take_128_head_items(scenario):
+    # a call that builds its own schedule counts query rows (one sequence of 300
+    # rows: 128-head items); the same call with a schedule from the metadata entry
+    # point counts sequences (64-head items); both against the oracle
+    from sparse_attn_sharedkv_amd import api, sparse_attn_sharedkv, sparse_attn_sharedkv_metadata
+    from oracle.gen import build_case
+
+    rows, d = 300, 576
+    _say(f"one sequence of {rows} rows, H=128, scenario {scenario}")
+    cfg = dict(scenario=scenario, layout_q="TND", B=1, S1=rows, T1=rows, N1=128, N2=1, D=d,
+               K=160 if scenario == 3 else 0, block_num1=-(-(rows + 700) // 64) + 2,
+               block_num2=max(1, -(-((rows + 700) // 4) // 64)) + 1, block_size1=64,
+               block_size2=64, cu_seqlens_q=[0, rows], seqused_kv=[rows + 700],
+               softmax_scale=1.0 / math.sqrt(d), cmp_ratio=4, ori_win_left=127,
+               ori_win_right=0, ori_mask_mode=4, cmp_mask_mode=3)
+    kw = build_case(cfg, torch.bfloat16, seed=900 + scenario)
+    kw["head_dim_v"] = 512
+    for key in ("q", "ori_kv", "cmp_kv"):
+        if kw.get(key) is not None:
+            kw[key] = (kw[key].float() * 0.05).to(torch.bfloat16)
+    dev = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+    assert api.prepare(**dev).args.m_base == 128
+    md = sparse_attn_sharedkv_metadata(
+        num_heads_q=128, num_heads_kv=1, head_dim=d, cu_seqlens_q=torch.tensor([0, rows]),
+        seqused_kv=kw["seqused_kv"], batch_size=1, max_seqlen_q=rows,
+        max_seqlen_kv=rows + 700, cmp_topk=cfg["K"], cmp_ratio=4, ori_win_left=127,
+        layout_q="TND", has_cmp_kv=scenario >= 2)
+    assert api.prepare(**dev, metadata=md).args.m_base == 64
+    okw = {k: v for k, v in kw.items() if k != "topk_cmp"}
+    ref, ref_lse = sparse_attn_oracle(**okw)
+    for extra in ({}, {"metadata": md.cuda()}):
+        out, lse = sparse_attn_sharedkv(**dev, return_softmax_lse=True, **extra)
+        torch.cuda.synchronize()
+        check_strict(out.cpu(), ref, lse.cpu(), ref_lse)

@@ -223,6 +223,12 @@ def test_item_size_rule_for_fp8_rows():
     assert M.m_base_for(64, batch=512, fp8_rows=True) == 64
     assert M.m_base_for(32, batch=512, fp8_rows=True) == 32
     assert M.m_base_for(128, item64=True, batch=512, fp8_rows=True) == 64
+    # a call's own schedule counts query rows (MTP: 64 sequences x 2 rows; prefill)
+    assert M.m_base_for(128, batch=64, rows=128) == 128
+    assert M.m_base_for(128, batch=1, rows=4096) == 128
+    assert M.m_base_for(128, batch=64, rows=64) == 64
+    assert M.m_base_for(128, batch=16, rows=32, fp8_rows=True) == 128
+    assert M.m_base_for(64, batch=1, rows=8192) == 64
     # the public entry point picks the size from the cache row format it is given
     lens = [3000] * 40
     common = dict(num_heads_q=128, num_heads_kv=1, head_dim=576,
