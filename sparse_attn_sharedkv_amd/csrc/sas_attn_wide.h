@@ -768,7 +768,9 @@ __global__ __launch_bounds__(512) void wide_kernel(const SasAttnArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[d][j] *= alpha;
         }
-        constexpr int VPF = FP8 ? 2 : SAS_WVPF;  // (fp8: two, making room for the dequantization)
+        // (fp8: two, making room for the dequantization; row pairs: two, measured
+        // faster there, while 128-head items keep three)
+        constexpr int VPF = (FP8 || PAIR) ? 2 : SAS_WVPF;
         typedef i16x4 SAS_LDS* lds4;
         const lds_p vbase = sb + wide_v(lane_id_here());
         auto vop = [&](int d) -> i16x8 {
